@@ -1,0 +1,124 @@
+// common.h - shared declarations of libsulimo_hip.so (host runtime + gfx950 kernels).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/sulimo_hip.h"
+
+// ---------------------------------------------------------------------------
+// Host-side objects behind the opaque C handles
+// ---------------------------------------------------------------------------
+struct sulimo_hip_ctx {
+  int device = 0;
+  bool shared = false;  // the get_or_init singleton (never freed)
+  hipStream_t stream = nullptr;
+  hipEvent_t done_event = nullptr;  // blocking-sync event used by sulimo_hip_wait
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  sulimo_hip_device_info info{};
+  // Prefill workspace (grown on demand): f32 residual stream, Q8_0 K/V staging
+  // for ring-wrapping ubatches, per-row argmax partials.
+  void *ws = nullptr;
+  size_t ws_bytes = 0;
+};
+
+struct sulimo_hip_buffer {
+  void *dev = nullptr;
+  void *host = nullptr;  // host mirror (the reference's arena slice), may be null
+  size_t bytes = 0;
+  bool read_only = false;
+  int device = 0;
+};
+
+namespace sulimo {
+
+// Thread-local last error; returns `code` for convenient `return fail(...)`.
+int32_t fail(int32_t code, const std::string &msg);
+int32_t hip_fail(hipError_t e, const char *what);
+// Grows ctx->ws to at least `bytes` (synchronizes the stream before freeing the old one).
+int32_t ensure_workspace(sulimo_hip_ctx *ctx, size_t bytes);
+
+#define SULIMO_HIP_TRY(call)                                   \
+  do {                                                         \
+    hipError_t e_ = (call);                                    \
+    if (e_ != hipSuccess) return ::sulimo::hip_fail(e_, #call); \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Kernel launchers (implemented in the .hip files; all enqueue on `s`)
+// ---------------------------------------------------------------------------
+
+// Epilogues of the Q4_0 x f16 GEMM.
+enum GemmEpilogue : int {
+  EPI_F16 = 0,     // out f16 [rows][ldo]
+  EPI_F32 = 1,     // out f32 [rows][ldo]
+  EPI_RESID = 2,   // out f32 residual [rows][ldo] += f16(acc)
+  EPI_SWIGLU = 3,  // out f16 [rows][ldo] = silu(acc_w0) * acc_w1 (w0 = gate, w1 = up)
+};
+
+// One weight matrix of a (possibly segmented) GEMM: `n` output rows, its
+// scales/quants, and where its outputs go (column offset `col0` in out, row stride ldo).
+struct GemmSegment {
+  const uint16_t *scales;
+  const uint8_t *quants;
+  void *out;
+  int n;
+  int ldo;
+  int col0;
+};
+
+struct GemmArgs {
+  const uint16_t *x;  // f16 [m][ldx]
+  int m, k, ldx;
+  int epi;
+  GemmSegment seg[3];
+  int nseg;
+  // EPI_SWIGLU: second weight matrix (up) with the same shape as seg[0] (gate).
+  const uint16_t *scales_up;
+  const uint8_t *quants_up;
+};
+
+int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s);
+
+// Bandwidth kernels (prefill_ops.hip).
+int32_t launch_rmsnorm_f16(const uint16_t *x, const float *w, uint16_t *out, int d, float eps,
+                           int n, hipStream_t s);
+int32_t launch_rmsnorm_f32(const float *x, const float *w, uint16_t *out, uint16_t *x16_out,
+                           int d, float eps, int n, hipStream_t s);
+int32_t launch_rope_f16(uint16_t *vec, int head_count, int head_dim, int rope_dim,
+                        float freq_base, int mode, int start_pos, int n, hipStream_t s);
+int32_t launch_kv_store_q8_0(const uint16_t *act, uint8_t *kv, int start_pos, int capacity,
+                             int blocks_per_pos, int n, hipStream_t s);
+int32_t launch_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t total,
+                        hipStream_t s);
+int32_t launch_add_f16(uint16_t *a, const uint16_t *b, size_t total, hipStream_t s);
+int32_t launch_f16_to_f32(const uint16_t *in, float *out, size_t total, hipStream_t s);
+int32_t launch_embed_q4_0(const uint16_t *scales, const uint8_t *quants, const uint32_t *tokens,
+                          int n, int embd, uint16_t *x, hipStream_t s);
+// RoPE on q (in place, f16) and k (f32 rotation), then Q8_0 of k and v into
+// k_dst/v_dst rows of `dst_stride` bytes; row t goes to slot (slot0 + t) % wrap.
+int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v, int n_head,
+                              int n_head_kv, int head_dim, int rope_dim, float freq_base,
+                              int mode, int start_pos, int n, uint8_t *k_dst, uint8_t *v_dst,
+                              int slot0, int wrap, hipStream_t s);
+// Copies n rows of `row_bytes` from src to ring slots (slot0 + t) % capacity.
+int32_t launch_ring_commit(const uint8_t *src, uint8_t *ring, size_t row_bytes, int slot0,
+                           int capacity, int n, hipStream_t s);
+int32_t launch_argmax_rows(const float *logits, int rows, int cols, int32_t *out, hipStream_t s);
+
+// Causal GQA attention over the Q8_0 ring (attention.hip). Keys at positions
+// p < new_pos0 are read from the ring at slot p % capacity; p >= new_pos0 from
+// `new_k/new_v` row (p - new_pos0) (row stride bytes_per_pos).
+struct AttnArgs {
+  const uint16_t *q;  // f16 [n][n_head][head_dim]
+  uint16_t *out;      // f16 [n][n_head][head_dim]
+  const uint8_t *k_ring, *v_ring;
+  const uint8_t *new_k, *new_v;
+  long new_pos0;
+  int start_pos, n, capacity, n_head, n_head_kv, head_dim;
+};
+int32_t launch_attention(const AttnArgs &a, hipStream_t s);
+
+}  // namespace sulimo

@@ -1,0 +1,512 @@
+// prefill.hip - C ABI of the per-op enqueue calls and of the whole-ubatch prefill.
+//
+// Mirrors crates/sulimo-ocl/src/prefill.rs (enqueue_* :67-330,
+// execute_prefill_ubatch :337-566) and crates/sulimo-ocl/src/gemm.rs:28-102.
+// Every call checks buffer sizes against the shapes on the host before it
+// enqueues anything, so a bad argument becomes SULIMO_HIP_ERR_INVALID_ARGUMENT
+// instead of an out-of-bounds device access.
+#include <limits.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "common.h"
+
+using namespace sulimo;
+
+namespace {
+
+constexpr int32_t kInval = SULIMO_HIP_ERR_INVALID_ARGUMENT;
+
+bool too_small(const sulimo_hip_buffer *b, size_t need, const char *name, int32_t *rc) {
+  if (!b) {
+    *rc = fail(kInval, std::string(name) + " buffer is null");
+    return true;
+  }
+  if (b->bytes < need) {
+    *rc = fail(kInval, std::string(name) + " buffer holds " + std::to_string(b->bytes) +
+                           " bytes, needs " + std::to_string(need));
+    return true;
+  }
+  return false;
+}
+
+#define NEED(buf, bytes, name)                      \
+  do {                                              \
+    int32_t rc_;                                    \
+    if (too_small((buf), (bytes), (name), &rc_)) return rc_; \
+  } while (0)
+
+template <typename T>
+T *dp(const sulimo_hip_buffer *b) {
+  return reinterpret_cast<T *>(b->dev);
+}
+
+bool fits_int(size_t v) { return v <= (size_t)INT_MAX; }
+
+int32_t begin(sulimo_hip_ctx *ctx) {
+  if (!ctx) return fail(kInval, "ctx is null");
+  SULIMO_HIP_TRY(hipSetDevice(ctx->device));
+  return SULIMO_HIP_OK;
+}
+
+// Small on-demand device buffer for token ids (separate from the workspace).
+struct TokenBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+  int device = -1;
+};
+thread_local TokenBuf g_tok;
+
+int32_t gemm_plain(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
+                   const sulimo_hip_buffer *quants, const void *x, void *out, size_t m, size_t k,
+                   size_t n, int epi) {
+  GemmArgs a{};
+  a.x = reinterpret_cast<const uint16_t *>(x);
+  a.m = (int)n;
+  a.k = (int)k;
+  a.ldx = (int)k;
+  a.epi = epi;
+  a.seg[0] = GemmSegment{dp<const uint16_t>(scales), dp<const uint8_t>(quants), out, (int)m, (int)m, 0};
+  a.nseg = 1;
+  return launch_gemm_q4_0(a, ctx->stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t sulimo_hip_enqueue_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
+                                         const sulimo_hip_buffer *quants,
+                                         const sulimo_hip_buffer *x, sulimo_hip_buffer *out,
+                                         size_t m, size_t k, size_t n) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (k == 0 || k % 32 != 0) return fail(kInval, "K must be a multiple of 32 (Q4_0 block size)");
+  if (m == 0 || m % 8 != 0) return fail(kInval, "M must be a multiple of 8");
+  if (!fits_int(m) || !fits_int(k) || !fits_int(n)) return fail(kInval, "GEMM dimension too large");
+  NEED(scales, m * (k / 32) * 2, "scales");
+  NEED(quants, m * (k / 32) * 16, "quants");
+  NEED(x, n * k * 2, "x");
+  NEED(out, n * m * 2, "out");
+  if (n == 0) return SULIMO_HIP_OK;
+  return gemm_plain(ctx, scales, quants, x->dev, out->dev, m, k, n, EPI_F16);
+}
+
+int32_t sulimo_hip_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
+                                 const sulimo_hip_buffer *quants, const sulimo_hip_buffer *x,
+                                 sulimo_hip_buffer *out, size_t m, size_t k, size_t n,
+                                 sulimo_hip_gemm_profile *profile) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if ((rc = sulimo_hip_timer_start(ctx))) return rc;
+  if ((rc = sulimo_hip_enqueue_gemm_q4_0_f16(ctx, scales, quants, x, out, m, k, n))) return rc;
+  float ms = 0.0f;
+  if ((rc = sulimo_hip_timer_stop(ctx, &ms))) return rc;
+  if ((rc = sulimo_hip_wait(ctx))) return rc;
+  if (profile) {
+    profile->duration_seconds = ms * 1e-3;
+    profile->gflops = ms > 0 ? 2.0 * m * n * k / (ms * 1e-3) / 1e9 : 0.0;
+    profile->kernel_variant = "gfx950-mfma-f16-q4_0";
+  }
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_enqueue_rmsnorm(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *x,
+                                   const sulimo_hip_buffer *w, sulimo_hip_buffer *out, size_t d,
+                                   float eps, size_t n) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (d == 0 || !fits_int(d) || !fits_int(n)) return fail(kInval, "bad rmsnorm shape");
+  NEED(x, n * d * 2, "x");
+  NEED(w, d * 4, "w");
+  NEED(out, n * d * 2, "out");
+  return launch_rmsnorm_f16(dp<const uint16_t>(x), dp<const float>(w), dp<uint16_t>(out), (int)d,
+                            eps, (int)n, ctx->stream);
+}
+
+int32_t sulimo_hip_enqueue_rope(sulimo_hip_ctx *ctx, sulimo_hip_buffer *vec, size_t head_count,
+                                size_t head_dim, size_t rope_dim, float freq_base, int32_t mode,
+                                size_t start_pos, size_t n) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (rope_dim > head_dim || rope_dim % 2 != 0) return fail(kInval, "rope_dim must be even and <= head_dim");
+  if (mode != 0 && mode != 1) return fail(kInval, "rope mode must be 0 (Norm) or 1 (NeoX)");
+  if (!fits_int(head_count * head_dim) || !fits_int(start_pos + n)) return fail(kInval, "rope shape too large");
+  NEED(vec, n * head_count * head_dim * 2, "vec");
+  return launch_rope_f16(dp<uint16_t>(vec), (int)head_count, (int)head_dim, (int)rope_dim,
+                         freq_base, mode, (int)start_pos, (int)n, ctx->stream);
+}
+
+int32_t sulimo_hip_enqueue_kv_store(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *act,
+                                    sulimo_hip_buffer *kv_cache, size_t start_pos,
+                                    size_t capacity, size_t blocks_per_pos, size_t n) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (capacity == 0 || blocks_per_pos == 0) return fail(kInval, "capacity and blocks_per_pos must be positive");
+  if (!fits_int(start_pos + n) || !fits_int(capacity)) return fail(kInval, "kv_store shape too large");
+  NEED(act, n * blocks_per_pos * 32 * 2, "act");
+  NEED(kv_cache, capacity * blocks_per_pos * 34, "kv_cache");
+  return launch_kv_store_q8_0(dp<const uint16_t>(act), dp<uint8_t>(kv_cache), (int)start_pos,
+                              (int)capacity, (int)blocks_per_pos, (int)n, ctx->stream);
+}
+
+int32_t sulimo_hip_enqueue_attention_prefill(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *q,
+                                             const sulimo_hip_buffer *k_cache,
+                                             const sulimo_hip_buffer *v_cache,
+                                             sulimo_hip_buffer *out, size_t start_pos,
+                                             size_t capacity, size_t head_count,
+                                             size_t head_count_kv, size_t head_dim, size_t n) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (head_dim % 32 != 0 || head_count_kv == 0 || head_count % head_count_kv != 0 || capacity == 0)
+    return fail(kInval, "attention needs head_dim % 32 == 0, head_count % head_count_kv == 0, capacity > 0");
+  if (!fits_int(start_pos + n) || !fits_int(capacity)) return fail(kInval, "attention shape too large");
+  const size_t bpp = head_count_kv * (head_dim / 32) * 34;
+  NEED(q, n * head_count * head_dim * 2, "q");
+  NEED(out, n * head_count * head_dim * 2, "out");
+  NEED(k_cache, capacity * bpp, "k_cache");
+  NEED(v_cache, capacity * bpp, "v_cache");
+  AttnArgs a{};
+  a.q = dp<const uint16_t>(q);
+  a.out = dp<uint16_t>(out);
+  a.k_ring = dp<const uint8_t>(k_cache);
+  a.v_ring = dp<const uint8_t>(v_cache);
+  a.new_k = a.new_v = nullptr;
+  a.new_pos0 = LONG_MAX;
+  a.start_pos = (int)start_pos;
+  a.n = (int)n;
+  a.capacity = (int)capacity;
+  a.n_head = (int)head_count;
+  a.n_head_kv = (int)head_count_kv;
+  a.head_dim = (int)head_dim;
+  return launch_attention(a, ctx->stream);
+}
+
+int32_t sulimo_hip_enqueue_silu_mul(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *gate,
+                                    const sulimo_hip_buffer *up, sulimo_hip_buffer *out,
+                                    size_t total_elements) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  NEED(gate, total_elements * 2, "gate");
+  NEED(up, total_elements * 2, "up");
+  NEED(out, total_elements * 2, "out");
+  return launch_silu_mul(dp<const uint16_t>(gate), dp<const uint16_t>(up), dp<uint16_t>(out),
+                         total_elements, ctx->stream);
+}
+
+int32_t sulimo_hip_enqueue_add(sulimo_hip_ctx *ctx, sulimo_hip_buffer *a,
+                               const sulimo_hip_buffer *b, size_t total_elements) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  NEED(a, total_elements * 2, "a");
+  NEED(b, total_elements * 2, "b");
+  return launch_add_f16(dp<uint16_t>(a), dp<const uint16_t>(b), total_elements, ctx->stream);
+}
+
+int32_t sulimo_hip_enqueue_logits_final(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *x_all,
+                                        const sulimo_hip_buffer *scales,
+                                        const sulimo_hip_buffer *quants, sulimo_hip_buffer *logits,
+                                        size_t vocab_size, size_t embd_dim, size_t token_idx) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (embd_dim == 0 || embd_dim % 32 != 0) return fail(kInval, "embd_dim must be a multiple of 32");
+  if (vocab_size == 0 || !fits_int(vocab_size) || !fits_int(embd_dim)) return fail(kInval, "bad vocab size");
+  NEED(x_all, (token_idx + 1) * embd_dim * 2, "x_all");
+  NEED(scales, vocab_size * (embd_dim / 32) * 2, "scales");
+  NEED(quants, vocab_size * (embd_dim / 32) * 16, "quants");
+  NEED(logits, vocab_size * 4, "logits");
+  const char *xrow = reinterpret_cast<const char *>(x_all->dev) + token_idx * embd_dim * 2;
+  return gemm_plain(ctx, scales, quants, xrow, logits->dev, vocab_size, embd_dim, 1, EPI_F32);
+}
+
+int32_t sulimo_hip_embed_tokens(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *embd_scales,
+                                const sulimo_hip_buffer *embd_quants, const uint32_t *tokens,
+                                size_t n, size_t embd, size_t vocab, sulimo_hip_buffer *x) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (embd == 0 || embd % 32 != 0 || !fits_int(embd) || !fits_int(n)) return fail(kInval, "embd must be a multiple of 32");
+  if (n == 0) return SULIMO_HIP_OK;
+  if (!tokens) return fail(kInval, "tokens is null");
+  for (size_t t = 0; t < n; t++)
+    if (tokens[t] >= vocab) return fail(kInval, "token id " + std::to_string(tokens[t]) + " >= vocab");
+  NEED(embd_scales, vocab * (embd / 32) * 2, "embd_scales");
+  NEED(embd_quants, vocab * (embd / 32) * 16, "embd_quants");
+  NEED(x, n * embd * 2, "x");
+  if (g_tok.bytes < n * 4 || g_tok.device != ctx->device) {
+    if (g_tok.p) {
+      SULIMO_HIP_TRY(hipStreamSynchronize(ctx->stream));
+      hipFree(g_tok.p);
+      g_tok.p = nullptr;
+      g_tok.bytes = 0;
+    }
+    size_t sz = ((n * 4) + 4095) & ~(size_t)4095;
+    SULIMO_HIP_TRY(hipMalloc(&g_tok.p, sz));
+    g_tok.bytes = sz;
+    g_tok.device = ctx->device;
+  }
+  SULIMO_HIP_TRY(hipMemcpyAsync(g_tok.p, tokens, n * 4, hipMemcpyHostToDevice, ctx->stream));
+  return launch_embed_q4_0(dp<const uint16_t>(embd_scales), dp<const uint8_t>(embd_quants),
+                           reinterpret_cast<const uint32_t *>(g_tok.p), (int)n, (int)embd,
+                           dp<uint16_t>(x), ctx->stream);
+}
+
+// ---- KV hand-over ----
+
+static int32_t kv_sync(sulimo_hip_ctx *ctx, const sulimo_hip_kv_cache *kv, size_t start_pos,
+                       size_t n, bool to_host) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (!kv || !kv->k_buffers || !kv->v_buffers || kv->capacity == 0 || kv->head_dim % 32 != 0)
+    return fail(kInval, "bad kv cache descriptor");
+  const size_t bpp = kv->head_count_kv * (kv->head_dim / 32) * 34;
+  const size_t cap = kv->capacity;
+  if (n == 0) return SULIMO_HIP_OK;
+  size_t segs[2][2];  // (first slot, count)
+  int ns = 0;
+  if (n >= cap) {
+    segs[0][0] = 0;
+    segs[0][1] = cap;
+    ns = 1;
+  } else {
+    size_t a = start_pos % cap;
+    size_t first = std::min(n, cap - a);
+    segs[ns][0] = a;
+    segs[ns++][1] = first;
+    if (first < n) {
+      segs[ns][0] = 0;
+      segs[ns++][1] = n - first;
+    }
+  }
+  for (int l = 0; l < kv->n_layers; l++) {
+    for (int which = 0; which < 2; which++) {
+      sulimo_hip_buffer *b = which ? kv->v_buffers[l] : kv->k_buffers[l];
+      NEED(b, cap * bpp, "kv layer");
+      if (!b->host) return fail(SULIMO_HIP_ERR_ZERO_COPY, "kv buffer has no host mirror");
+      for (int s = 0; s < ns; s++) {
+        char *dev = (char *)b->dev + segs[s][0] * bpp;
+        char *host = (char *)b->host + segs[s][0] * bpp;
+        size_t bytes = segs[s][1] * bpp;
+        if (to_host)
+          SULIMO_HIP_TRY(hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+        else
+          SULIMO_HIP_TRY(hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, ctx->stream));
+      }
+    }
+  }
+  if (to_host) return sulimo_hip_wait(ctx);
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_kv_sync_to_host(sulimo_hip_ctx *ctx, const sulimo_hip_kv_cache *kv,
+                                   size_t start_pos, size_t n) {
+  return kv_sync(ctx, kv, start_pos, n, true);
+}
+
+int32_t sulimo_hip_kv_sync_from_host(sulimo_hip_ctx *ctx, const sulimo_hip_kv_cache *kv,
+                                     size_t start_pos, size_t n) {
+  return kv_sync(ctx, kv, start_pos, n, false);
+}
+
+// ---- whole-ubatch prefill ----
+
+int32_t sulimo_hip_execute_prefill_ubatch_ex(
+    sulimo_hip_ctx *ctx, const sulimo_hip_model_config *cfg,
+    const sulimo_hip_model_tensors *tensors, sulimo_hip_kv_cache *kv,
+    sulimo_hip_prefill_scratch *scratch, size_t start_pos, size_t n,
+    const sulimo_hip_prefill_outputs *outputs) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (!cfg || !tensors || !kv || !scratch) return fail(kInval, "null argument");
+  if (n == 0) return SULIMO_HIP_OK;
+  const size_t D = cfg->embd, F = cfg->ffn, Hq = cfg->n_head, Hkv = cfg->n_head_kv,
+               hd = cfg->head_dim, V = cfg->vocab, L = cfg->n_layers;
+  const size_t qd = Hq * hd, kvd = Hkv * hd;
+  const size_t cap = kv->capacity;
+  if (D == 0 || D % 32 || F == 0 || F % 32 || qd % 32 || kvd % 32 || Hkv == 0 || Hq % Hkv ||
+      (hd != 64 && hd != 128) || V == 0 || L == 0)
+    return fail(kInval, "unsupported model shape (needs dims % 32 == 0, head_dim 64 or 128, head_count % head_count_kv == 0)");
+  if (cfg->rope_dim < 0 || (size_t)cfg->rope_dim > hd || cfg->rope_dim % 2 || (cfg->rope_mode != 0 && cfg->rope_mode != 1))
+    return fail(kInval, "bad rope configuration");
+  if (tensors->n_layers != (int)L || kv->n_layers != (int)L || !tensors->layers || !kv->k_buffers || !kv->v_buffers)
+    return fail(kInval, "layer count mismatch");
+  if (kv->head_count_kv != Hkv || kv->head_dim != hd || cap == 0) return fail(kInval, "kv cache shape mismatch");
+  if (n > scratch->max_n) return fail(kInval, "n exceeds scratch.max_n");
+  if (!fits_int(start_pos + n) || !fits_int(cap) || !fits_int(V * D)) return fail(kInval, "shape too large");
+  const size_t bpp = Hkv * (hd / 32) * 34;
+  const size_t nbD = D / 32, nbF = F / 32, nbQ = qd / 32;
+  NEED(scratch->x, n * D * 2, "scratch.x");
+  NEED(scratch->h, n * D * 2, "scratch.h");
+  NEED(scratch->q, n * qd * 2, "scratch.q");
+  NEED(scratch->k, n * kvd * 2, "scratch.k");
+  NEED(scratch->v, n * kvd * 2, "scratch.v");
+  NEED(scratch->attn_out, n * qd * 2, "scratch.attn_out");
+  NEED(scratch->ffn_swiglu, n * F * 2, "scratch.ffn_swiglu");
+  NEED(scratch->logits, V * 4, "scratch.logits");
+  NEED(tensors->output_norm, D * 4, "output_norm");
+  NEED(tensors->output_scales, V * nbD * 2, "output_scales");
+  NEED(tensors->output_quants, V * nbD * 16, "output_quants");
+  for (size_t l = 0; l < L; l++) {
+    const sulimo_hip_layer_tensors &T = tensors->layers[l];
+    NEED(T.attn_norm, D * 4, "attn_norm");
+    NEED(T.ffn_norm, D * 4, "ffn_norm");
+    NEED(T.attn_q_scales, qd * nbD * 2, "attn_q_scales");
+    NEED(T.attn_q_quants, qd * nbD * 16, "attn_q_quants");
+    NEED(T.attn_k_scales, kvd * nbD * 2, "attn_k_scales");
+    NEED(T.attn_k_quants, kvd * nbD * 16, "attn_k_quants");
+    NEED(T.attn_v_scales, kvd * nbD * 2, "attn_v_scales");
+    NEED(T.attn_v_quants, kvd * nbD * 16, "attn_v_quants");
+    NEED(T.attn_out_scales, D * nbQ * 2, "attn_out_scales");
+    NEED(T.attn_out_quants, D * nbQ * 16, "attn_out_quants");
+    NEED(T.ffn_gate_scales, F * nbD * 2, "ffn_gate_scales");
+    NEED(T.ffn_gate_quants, F * nbD * 16, "ffn_gate_quants");
+    NEED(T.ffn_up_scales, F * nbD * 2, "ffn_up_scales");
+    NEED(T.ffn_up_quants, F * nbD * 16, "ffn_up_quants");
+    NEED(T.ffn_down_scales, D * nbF * 2, "ffn_down_scales");
+    NEED(T.ffn_down_quants, D * nbF * 16, "ffn_down_quants");
+    NEED(kv->k_buffers[l], cap * bpp, "kv k");
+    NEED(kv->v_buffers[l], cap * bpp, "kv v");
+  }
+  if (outputs && outputs->logits_all) NEED(outputs->logits_all, n * V * 4, "logits_all");
+  if (outputs && outputs->argmax_all) NEED(outputs->argmax_all, n * 4, "argmax_all");
+
+  // Workspace: f32 residual [n][D] | staged K codes [n][bpp] | staged V codes | argmax logits chunk.
+  const bool staged = start_pos + n > cap;
+  const size_t off_k = (n * D * 4 + 255) & ~(size_t)255;
+  const size_t off_v = off_k + ((staged ? n * bpp : 0) + 255 & ~(size_t)255);
+  const size_t off_l = off_v + ((staged ? n * bpp : 0) + 255 & ~(size_t)255);
+  const bool want_argmax = outputs && outputs->argmax_all;
+  const bool own_logits = want_argmax && !outputs->logits_all;
+  const size_t chunk_rows = 256;
+  const size_t ws_need = off_l + (own_logits ? chunk_rows * V * 4 : 0);
+  if ((rc = ensure_workspace(ctx, ws_need))) return rc;
+  char *ws = reinterpret_cast<char *>(ctx->ws);
+  float *xres = reinterpret_cast<float *>(ws);
+  uint8_t *stg_k = reinterpret_cast<uint8_t *>(ws + off_k);
+  uint8_t *stg_v = reinterpret_cast<uint8_t *>(ws + off_v);
+  hipStream_t s = ctx->stream;
+  const int in = (int)n;
+
+  if ((rc = launch_f16_to_f32(dp<const uint16_t>(scratch->x), xres, n * D, s))) return rc;
+  for (size_t l = 0; l < L; l++) {
+    const sulimo_hip_layer_tensors &T = tensors->layers[l];
+    uint8_t *ring_k = dp<uint8_t>(kv->k_buffers[l]);
+    uint8_t *ring_v = dp<uint8_t>(kv->v_buffers[l]);
+    // 1. attention RMSNorm
+    if ((rc = launch_rmsnorm_f32(xres, dp<const float>(T.attn_norm), dp<uint16_t>(scratch->h), nullptr,
+                                 (int)D, cfg->eps, in, s)))
+      return rc;
+    // 2. q, k, v projections as one segmented GEMM
+    GemmArgs g{};
+    g.x = dp<const uint16_t>(scratch->h);
+    g.m = in;
+    g.k = (int)D;
+    g.ldx = (int)D;
+    g.epi = EPI_F16;
+    g.seg[0] = GemmSegment{dp<const uint16_t>(T.attn_q_scales), dp<const uint8_t>(T.attn_q_quants), scratch->q->dev, (int)qd, (int)qd, 0};
+    g.seg[1] = GemmSegment{dp<const uint16_t>(T.attn_k_scales), dp<const uint8_t>(T.attn_k_quants), scratch->k->dev, (int)kvd, (int)kvd, 0};
+    g.seg[2] = GemmSegment{dp<const uint16_t>(T.attn_v_scales), dp<const uint8_t>(T.attn_v_quants), scratch->v->dev, (int)kvd, (int)kvd, 0};
+    g.nseg = 3;
+    if ((rc = launch_gemm_q4_0(g, s))) return rc;
+    // 3-4. RoPE on q and k, Q8_0 of k and v into the ring (or staging when wrapping)
+    if ((rc = launch_rope_qkv_store(dp<uint16_t>(scratch->q), dp<const uint16_t>(scratch->k),
+                                    dp<const uint16_t>(scratch->v), (int)Hq, (int)Hkv, (int)hd,
+                                    cfg->rope_dim, cfg->rope_base, cfg->rope_mode, (int)start_pos, in,
+                                    staged ? stg_k : ring_k, staged ? stg_v : ring_v,
+                                    staged ? 0 : (int)(start_pos % cap), staged ? in : (int)cap, s)))
+      return rc;
+    // 5. causal GQA attention
+    AttnArgs at{};
+    at.q = dp<const uint16_t>(scratch->q);
+    at.out = dp<uint16_t>(scratch->attn_out);
+    at.k_ring = ring_k;
+    at.v_ring = ring_v;
+    at.new_k = staged ? stg_k : nullptr;
+    at.new_v = staged ? stg_v : nullptr;
+    at.new_pos0 = staged ? (long)start_pos : LONG_MAX;
+    at.start_pos = (int)start_pos;
+    at.n = in;
+    at.capacity = (int)cap;
+    at.n_head = (int)Hq;
+    at.n_head_kv = (int)Hkv;
+    at.head_dim = (int)hd;
+    if ((rc = launch_attention(at, s))) return rc;
+    if (staged) {
+      const size_t keep = std::min(n, cap);
+      const size_t first = n - keep;
+      if ((rc = launch_ring_commit(stg_k + first * bpp, ring_k, bpp, (int)((start_pos + first) % cap), (int)cap, (int)keep, s))) return rc;
+      if ((rc = launch_ring_commit(stg_v + first * bpp, ring_v, bpp, (int)((start_pos + first) % cap), (int)cap, (int)keep, s))) return rc;
+    }
+    // 6-7. output projection, residual add fused: x += f16(Wo a)
+    GemmArgs go{};
+    go.x = dp<const uint16_t>(scratch->attn_out);
+    go.m = in;
+    go.k = (int)qd;
+    go.ldx = (int)qd;
+    go.epi = EPI_RESID;
+    go.seg[0] = GemmSegment{dp<const uint16_t>(T.attn_out_scales), dp<const uint8_t>(T.attn_out_quants), xres, (int)D, (int)D, 0};
+    go.nseg = 1;
+    if ((rc = launch_gemm_q4_0(go, s))) return rc;
+    // 8. FFN RMSNorm
+    if ((rc = launch_rmsnorm_f32(xres, dp<const float>(T.ffn_norm), dp<uint16_t>(scratch->h), nullptr,
+                                 (int)D, cfg->eps, in, s)))
+      return rc;
+    // 9-10. gate and up projections with SwiGLU fused into the epilogue
+    GemmArgs gu{};
+    gu.x = dp<const uint16_t>(scratch->h);
+    gu.m = in;
+    gu.k = (int)D;
+    gu.ldx = (int)D;
+    gu.epi = EPI_SWIGLU;
+    gu.seg[0] = GemmSegment{dp<const uint16_t>(T.ffn_gate_scales), dp<const uint8_t>(T.ffn_gate_quants), scratch->ffn_swiglu->dev, (int)F, (int)F, 0};
+    gu.nseg = 1;
+    gu.scales_up = dp<const uint16_t>(T.ffn_up_scales);
+    gu.quants_up = dp<const uint8_t>(T.ffn_up_quants);
+    if ((rc = launch_gemm_q4_0(gu, s))) return rc;
+    // 11-12. down projection, residual add fused
+    GemmArgs gd{};
+    gd.x = dp<const uint16_t>(scratch->ffn_swiglu);
+    gd.m = in;
+    gd.k = (int)F;
+    gd.ldx = (int)F;
+    gd.epi = EPI_RESID;
+    gd.seg[0] = GemmSegment{dp<const uint16_t>(T.ffn_down_scales), dp<const uint8_t>(T.ffn_down_quants), xres, (int)D, (int)D, 0};
+    gd.nseg = 1;
+    if ((rc = launch_gemm_q4_0(gd, s))) return rc;
+  }
+  // 13. output RMSNorm of all n rows (h), final residual back to scratch.x as f16
+  if ((rc = launch_rmsnorm_f32(xres, dp<const float>(tensors->output_norm), dp<uint16_t>(scratch->h),
+                               dp<uint16_t>(scratch->x), (int)D, cfg->eps, in, s)))
+    return rc;
+  // 14. logits of the last token
+  const char *hlast = reinterpret_cast<const char *>(scratch->h->dev) + (n - 1) * D * 2;
+  if ((rc = gemm_plain(ctx, tensors->output_scales, tensors->output_quants, hlast, scratch->logits->dev, V, D, 1, EPI_F32)))
+    return rc;
+  // Optional per-position logits / top-1.
+  if (outputs && (outputs->logits_all || outputs->argmax_all)) {
+    for (size_t r0 = 0; r0 < n; r0 += (outputs->logits_all ? n : chunk_rows)) {
+      const size_t rows = outputs->logits_all ? n : std::min(chunk_rows, n - r0);
+      float *lg = outputs->logits_all ? dp<float>(outputs->logits_all) + r0 * V
+                                      : reinterpret_cast<float *>(ws + off_l);
+      const char *hx = reinterpret_cast<const char *>(scratch->h->dev) + r0 * D * 2;
+      if ((rc = gemm_plain(ctx, tensors->output_scales, tensors->output_quants, hx, lg, V, D, rows, EPI_F32))) return rc;
+      if (want_argmax &&
+          (rc = launch_argmax_rows(lg, (int)rows, (int)V, dp<int32_t>(outputs->argmax_all) + r0, s)))
+        return rc;
+    }
+  }
+  // 15. one blocking wait for the whole ubatch
+  return sulimo_hip_wait(ctx);
+}
+
+int32_t sulimo_hip_execute_prefill_ubatch(sulimo_hip_ctx *ctx, const sulimo_hip_model_config *cfg,
+                                          const sulimo_hip_model_tensors *tensors,
+                                          sulimo_hip_kv_cache *kv_cache,
+                                          sulimo_hip_prefill_scratch *scratch, size_t start_pos,
+                                          size_t n) {
+  return sulimo_hip_execute_prefill_ubatch_ex(ctx, cfg, tensors, kv_cache, scratch, start_pos, n,
+                                              nullptr);
+}
+
+}  // extern "C"

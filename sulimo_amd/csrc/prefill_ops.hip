@@ -1,0 +1,359 @@
+// prefill_ops.hip - HBM-bound prefill kernels for gfx950 (wave64 reductions).
+//
+// Reference formulas: kernels/prefill.cl (rmsnorm_f16_f32w :4-29, rope_f16 :32-68,
+// kv_store_q8_0 :72-116, silu_mul_f16 :240-253, add_f16 :256-266) and the host
+// embedding gather of crates/sulimo-engine/src/scheduler.rs:329-374.
+#include "common.h"
+
+namespace sulimo {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+// Max over the 32 lanes of a half-wave (one Q8_0 block).
+__device__ __forceinline__ float half_wave_max(float v) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float load_f(const _Float16 *p, size_t i) { return (float)p[i]; }
+__device__ __forceinline__ float load_f(const float *p, size_t i) { return p[i]; }
+
+// One wave per row: out = f16(x * (1/sqrt(mean(x^2)+eps)) * w).
+// With x16_out, also writes f16(x) (final residual hand-back).
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const T *__restrict__ x,
+                                                      const float *__restrict__ w,
+                                                      _Float16 *__restrict__ out,
+                                                      _Float16 *__restrict__ x16_out, int d,
+                                                      float eps, int n) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n) return;
+  const T *xr = x + (size_t)row * d;
+  float ss = 0.0f;
+  for (int i = lane; i < d; i += 64) {
+    float v = load_f(xr, i);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  const float scale = 1.0f / sqrtf(ss / (float)d + eps);
+  _Float16 *o = out + (size_t)row * d;
+  for (int i = lane; i < d; i += 64) {
+    float v = load_f(xr, i);
+    o[i] = (_Float16)(v * scale * w[i]);
+    if (x16_out) x16_out[(size_t)row * d + i] = (_Float16)v;
+  }
+}
+
+// Rotation angle of pair i at position pos: pos / base^(2i/rope_dim).
+__device__ __forceinline__ void rope_cs(int pos, int i, int rope_dim, float base, float &c,
+                                        float &s) {
+  float freq = 1.0f / powf(base, (float)(2 * i) / (float)rope_dim);
+  float theta = (float)pos * freq;
+  sincosf(theta, &s, &c);
+}
+
+// One thread per (token, head, pair): in-place f16 rotation.
+__global__ void rope_f16_kernel(_Float16 *vec, int head_count, int head_dim, int rope_dim,
+                                float base, int mode, int start_pos, int n) {
+  const int half = rope_dim / 2;
+  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long total = (long)n * head_count * half;
+  if (gid >= total) return;
+  const int i = (int)(gid % half);
+  const long th = gid / half;
+  const int h = (int)(th % head_count);
+  const int t = (int)(th / head_count);
+  _Float16 *hp = vec + ((size_t)t * head_count + h) * head_dim;
+  float c, s;
+  rope_cs(start_pos + t, i, rope_dim, base, c, s);
+  const int i0 = mode == 0 ? 2 * i : i;
+  const int i1 = mode == 0 ? 2 * i + 1 : i + half;
+  const float v0 = (float)hp[i0], v1 = (float)hp[i1];
+  hp[i0] = (_Float16)(v0 * c - v1 * s);
+  hp[i1] = (_Float16)(v0 * s + v1 * c);
+}
+
+// Q8_0 quantization of the 32 values held by the 32 lanes of a half-wave
+// (quantize_f32_to_q8_0, crates/sulimo-core/src/kv_cache.rs:162-193): d = amax/127,
+// f16 scale with RNE, id = 1/d (correctly rounded division), code = round-half-away.
+__device__ __forceinline__ void q8_block_store(float v, int e, uint8_t *blk) {
+  const float amax = half_wave_max(fabsf(v));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  float q = roundf(v * id);
+  q = fminf(fmaxf(q, -128.0f), 127.0f);
+  if (e == 0) *reinterpret_cast<_Float16 *>(blk) = (_Float16)d;
+  blk[2 + e] = (uint8_t)(int8_t)(int)q;
+}
+
+// Half-wave per (token, block).
+__global__ __launch_bounds__(256) void kv_store_kernel(const _Float16 *act, uint8_t *kv,
+                                                       int start_pos, int capacity,
+                                                       int blocks_per_pos, int n) {
+  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long bid = gid >> 5;
+  const int e = (int)(gid & 31);
+  const long nblk = (long)n * blocks_per_pos;
+  if (bid >= nblk) return;  // whole half-waves exit together (nblk*32 boundary)
+  const int t = (int)(bid / blocks_per_pos), b = (int)(bid % blocks_per_pos);
+  const int ring = (start_pos + t) % capacity;
+  const float v = (float)act[(size_t)bid * 32 + e];
+  q8_block_store(v, e, kv + ((size_t)ring * blocks_per_pos + b) * 34);
+}
+
+__global__ void silu_mul_kernel(const _Float16 *g, const _Float16 *u, _Float16 *out,
+                                size_t total) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const float gv = (float)g[i], uv = (float)u[i];
+  out[i] = (_Float16)(gv / (1.0f + expf(-gv)) * uv);
+}
+
+__global__ void add_f16_kernel(_Float16 *a, const _Float16 *b, size_t total) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  a[i] = (_Float16)((float)a[i] + (float)b[i]);
+}
+
+__global__ void f16_to_f32_kernel(const _Float16 *in, float *out, size_t total) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  out[i] = (float)in[i];
+}
+
+// One thread per (token, byte): x = f16(d * (q-8)) for the low and high nibble.
+__global__ void embed_q4_kernel(const uint16_t *scales, const uint8_t *quants,
+                                const uint32_t *tokens, int n, int embd, _Float16 *x) {
+  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int bytes_per_row = embd / 2;
+  if (gid >= (long)n * bytes_per_row) return;
+  const int t = (int)(gid / bytes_per_row);
+  const int byte = (int)(gid % bytes_per_row);
+  const int b = byte >> 4, i = byte & 15;
+  const size_t row = tokens[t];
+  const size_t bpr = embd / 32;
+  const float d = (float)__builtin_bit_cast(_Float16, scales[row * bpr + b]);
+  const uint8_t q = quants[(row * bpr + b) * 16 + i];
+  _Float16 *o = x + (size_t)t * embd + b * 32;
+  o[i] = (_Float16)(d * (float)((int)(q & 15) - 8));
+  o[16 + i] = (_Float16)(d * (float)((int)(q >> 4) - 8));
+}
+
+// One wave per (token, head slot). Slots [0, n_head) are q heads (rotated in
+// place, f16), [n_head, n_head+n_head_kv) k heads (rotated in f32, then Q8_0),
+// the rest v heads (Q8_0 of the f16 values). head_dim <= 256, multiple of 32.
+__global__ __launch_bounds__(256) void rope_qkv_store_kernel(
+    _Float16 *q, const _Float16 *k, const _Float16 *v, int n_head, int n_head_kv, int head_dim,
+    int rope_dim, float base, int mode, int start_pos, int n, uint8_t *k_dst, uint8_t *v_dst,
+    int slot0, int wrap) {
+  __shared__ float sh[4][256];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int slots = n_head + 2 * n_head_kv;
+  const long job = (long)blockIdx.x * 4 + wave;
+  if (job >= (long)n * slots) return;  // whole waves exit; no block barrier below
+  const int t = (int)(job / slots), hs = (int)(job % slots);
+  float *buf = sh[wave];
+  const int pos = start_pos + t;
+  const int half = rope_dim / 2;
+  const int kvd = n_head_kv * head_dim;
+  const size_t row_bytes = (size_t)n_head_kv * (head_dim / 32) * 34;
+  if (hs < n_head + n_head_kv) {
+    _Float16 *hp;
+    if (hs < n_head)
+      hp = q + ((size_t)t * n_head + hs) * head_dim;
+    else
+      hp = const_cast<_Float16 *>(k) + (size_t)t * kvd + (size_t)(hs - n_head) * head_dim;
+    for (int i = lane; i < head_dim; i += 64) buf[i] = (float)hp[i];
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < half; i += 64) {
+      float c, s;
+      rope_cs(pos, i, rope_dim, base, c, s);
+      const int i0 = mode == 0 ? 2 * i : i;
+      const int i1 = mode == 0 ? 2 * i + 1 : i + half;
+      const float v0 = buf[i0], v1 = buf[i1];
+      buf[i0] = v0 * c - v1 * s;
+      buf[i1] = v0 * s + v1 * c;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (hs < n_head) {
+      for (int i = lane; i < head_dim; i += 64) hp[i] = (_Float16)buf[i];
+      return;
+    }
+  } else {
+    const _Float16 *hp = v + (size_t)t * kvd + (size_t)(hs - n_head - n_head_kv) * head_dim;
+    for (int i = lane; i < head_dim; i += 64) buf[i] = (float)hp[i];
+    __builtin_amdgcn_wave_barrier();
+  }
+  const bool is_k = hs < n_head + n_head_kv;
+  const int kvh = is_k ? hs - n_head : hs - n_head - n_head_kv;
+  const int row = (int)(((long)slot0 + t) % wrap);
+  uint8_t *dst = (is_k ? k_dst : v_dst) + (size_t)row * row_bytes + (size_t)kvh * (head_dim / 32) * 34;
+  for (int i = lane; i < head_dim; i += 64) q8_block_store(buf[i], i & 31, dst + (i >> 5) * 34);
+}
+
+__global__ void ring_commit_kernel(const uint16_t *src, uint16_t *ring, size_t row_u16, int slot0,
+                                   int capacity, int n) {
+  const int t = blockIdx.x;
+  if (t >= n) return;
+  const size_t slot = ((size_t)slot0 + t) % capacity;
+  for (size_t i = threadIdx.x; i < row_u16; i += blockDim.x)
+    ring[slot * row_u16 + i] = src[(size_t)t * row_u16 + i];
+}
+
+// One workgroup per row; ties resolve to the highest index (Rust Iterator::max_by).
+__global__ __launch_bounds__(256) void argmax_kernel(const float *logits, int cols, int32_t *out) {
+  __shared__ float sv[256];
+  __shared__ int si[256];
+  const float *r = logits + (size_t)blockIdx.x * cols;
+  float bv = -INFINITY;
+  int bi = -1;
+  for (int i = threadIdx.x; i < cols; i += 256) {
+    float v = r[i];
+    if (v >= bv) {
+      bv = v;
+      bi = i;
+    }
+  }
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int o = 128; o >= 1; o >>= 1) {
+    if (threadIdx.x < o) {
+      float v2 = sv[threadIdx.x + o];
+      int i2 = si[threadIdx.x + o];
+      if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 > si[threadIdx.x])) {
+        sv[threadIdx.x] = v2;
+        si[threadIdx.x] = i2;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[blockIdx.x] = si[0];
+}
+
+inline int32_t check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, what);
+}
+inline unsigned blocks_for(size_t total, unsigned bs) { return (unsigned)((total + bs - 1) / bs); }
+
+}  // namespace
+
+int32_t launch_rmsnorm_f16(const uint16_t *x, const float *w, uint16_t *out, int d, float eps,
+                           int n, hipStream_t s) {
+  if (n <= 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel<_Float16>, dim3((n + 3) / 4), dim3(256), 0, s,
+                     reinterpret_cast<const _Float16 *>(x), w, reinterpret_cast<_Float16 *>(out),
+                     (_Float16 *)nullptr, d, eps, n);
+  return check_launch("rmsnorm_kernel<f16>");
+}
+
+int32_t launch_rmsnorm_f32(const float *x, const float *w, uint16_t *out, uint16_t *x16_out, int d,
+                           float eps, int n, hipStream_t s) {
+  if (n <= 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3((n + 3) / 4), dim3(256), 0, s, x, w,
+                     reinterpret_cast<_Float16 *>(out), reinterpret_cast<_Float16 *>(x16_out), d,
+                     eps, n);
+  return check_launch("rmsnorm_kernel<f32>");
+}
+
+int32_t launch_rope_f16(uint16_t *vec, int head_count, int head_dim, int rope_dim,
+                        float freq_base, int mode, int start_pos, int n, hipStream_t s) {
+  const size_t total = (size_t)n * head_count * (rope_dim / 2);
+  if (total == 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(rope_f16_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s,
+                     reinterpret_cast<_Float16 *>(vec), head_count, head_dim, rope_dim, freq_base,
+                     mode, start_pos, n);
+  return check_launch("rope_f16_kernel");
+}
+
+int32_t launch_kv_store_q8_0(const uint16_t *act, uint8_t *kv, int start_pos, int capacity,
+                             int blocks_per_pos, int n, hipStream_t s) {
+  // With n > capacity, tokens t and t+capacity share a slot and the later one wins
+  // (the sequential semantics of the host KvCache); write only the last `capacity`.
+  if (n > capacity) {
+    const int skip = n - capacity;
+    act += (size_t)skip * blocks_per_pos * 32;
+    start_pos += skip;
+    n = capacity;
+  }
+  const size_t total = (size_t)n * blocks_per_pos * 32;
+  if (total == 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(kv_store_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s,
+                     reinterpret_cast<const _Float16 *>(act), kv, start_pos, capacity,
+                     blocks_per_pos, n);
+  return check_launch("kv_store_kernel");
+}
+
+int32_t launch_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, size_t total,
+                        hipStream_t s) {
+  if (total == 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s,
+                     reinterpret_cast<const _Float16 *>(g), reinterpret_cast<const _Float16 *>(u),
+                     reinterpret_cast<_Float16 *>(out), total);
+  return check_launch("silu_mul_kernel");
+}
+
+int32_t launch_add_f16(uint16_t *a, const uint16_t *b, size_t total, hipStream_t s) {
+  if (total == 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(add_f16_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s,
+                     reinterpret_cast<_Float16 *>(a), reinterpret_cast<const _Float16 *>(b),
+                     total);
+  return check_launch("add_f16_kernel");
+}
+
+int32_t launch_f16_to_f32(const uint16_t *in, float *out, size_t total, hipStream_t s) {
+  if (total == 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(f16_to_f32_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s,
+                     reinterpret_cast<const _Float16 *>(in), out, total);
+  return check_launch("f16_to_f32_kernel");
+}
+
+int32_t launch_embed_q4_0(const uint16_t *scales, const uint8_t *quants, const uint32_t *tokens,
+                          int n, int embd, uint16_t *x, hipStream_t s) {
+  const size_t total = (size_t)n * (embd / 2);
+  if (total == 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(embed_q4_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, scales,
+                     quants, tokens, n, embd, reinterpret_cast<_Float16 *>(x));
+  return check_launch("embed_q4_kernel");
+}
+
+int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v, int n_head,
+                              int n_head_kv, int head_dim, int rope_dim, float freq_base,
+                              int mode, int start_pos, int n, uint8_t *k_dst, uint8_t *v_dst,
+                              int slot0, int wrap, hipStream_t s) {
+  if (head_dim > 256 || head_dim % 32 != 0)
+    return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "head_dim must be a multiple of 32 and <= 256");
+  const size_t jobs = (size_t)n * (n_head + 2 * n_head_kv);
+  if (jobs == 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(rope_qkv_store_kernel, dim3(blocks_for(jobs, 4)), dim3(256), 0, s,
+                     reinterpret_cast<_Float16 *>(q), reinterpret_cast<const _Float16 *>(k),
+                     reinterpret_cast<const _Float16 *>(v), n_head, n_head_kv, head_dim, rope_dim,
+                     freq_base, mode, start_pos, n, k_dst, v_dst, slot0, wrap);
+  return check_launch("rope_qkv_store_kernel");
+}
+
+int32_t launch_ring_commit(const uint8_t *src, uint8_t *ring, size_t row_bytes, int slot0,
+                           int capacity, int n, hipStream_t s) {
+  if (n <= 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(ring_commit_kernel, dim3(n), dim3(128), 0, s,
+                     reinterpret_cast<const uint16_t *>(src), reinterpret_cast<uint16_t *>(ring),
+                     row_bytes / 2, slot0, capacity, n);
+  return check_launch("ring_commit_kernel");
+}
+
+int32_t launch_argmax_rows(const float *logits, int rows, int cols, int32_t *out, hipStream_t s) {
+  if (rows <= 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, s, logits, cols, out);
+  return check_launch("argmax_kernel");
+}
+
+}  // namespace sulimo

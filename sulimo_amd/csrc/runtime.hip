@@ -1,0 +1,280 @@
+// runtime.hip - host runtime of libsulimo_hip.so: contexts, buffers, errors,
+// waiting, probing and timing. Replaces crates/sulimo-ocl/src/{program,buffer,
+// waiter,probe}.rs with HIP equivalents for one discrete MI355X device.
+#include <stdio.h>
+#include <string.h>
+
+#include <atomic>
+#include <mutex>
+#include <string>
+
+#include "common.h"
+
+namespace sulimo {
+
+static thread_local std::string g_last_error;
+static std::atomic<size_t> g_active_buffers{0};
+
+int32_t fail(int32_t code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int32_t hip_fail(hipError_t e, const char *what) {
+  std::string m = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+  int32_t code = SULIMO_HIP_ERR_DRIVER;
+  if (e == hipErrorNoDevice || e == hipErrorInvalidDevice) code = SULIMO_HIP_ERR_DEVICE_NOT_FOUND;
+  if (e == hipErrorNoBinaryForGpu || e == hipErrorInvalidImage || e == hipErrorInvalidKernelFile)
+    code = SULIMO_HIP_ERR_BUILD_FAILED;
+  if (e == hipErrorLaunchFailure || e == hipErrorIllegalAddress || e == hipErrorAssert ||
+      e == hipErrorLaunchTimeOut)
+    code = SULIMO_HIP_ERR_EXECUTION_FAILED;
+  return fail(code, m);
+}
+
+int32_t ensure_workspace(sulimo_hip_ctx *ctx, size_t bytes) {
+  if (ctx->ws_bytes >= bytes) return SULIMO_HIP_OK;
+  SULIMO_HIP_TRY(hipSetDevice(ctx->device));
+  if (ctx->ws) {
+    SULIMO_HIP_TRY(hipStreamSynchronize(ctx->stream));
+    SULIMO_HIP_TRY(hipFree(ctx->ws));
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+  }
+  size_t sz = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+  SULIMO_HIP_TRY(hipMalloc(&ctx->ws, sz));
+  ctx->ws_bytes = sz;
+  return SULIMO_HIP_OK;
+}
+
+static int32_t fill_info(int device, sulimo_hip_device_info *info) {
+  hipDeviceProp_t p;
+  SULIMO_HIP_TRY(hipGetDeviceProperties(&p, device));
+  memset(info, 0, sizeof(*info));
+  snprintf(info->device_name, sizeof(info->device_name), "%s", p.name);
+  snprintf(info->arch_name, sizeof(info->arch_name), "%s", p.gcnArchName);
+  int drv = 0;
+  hipDriverGetVersion(&drv);
+  snprintf(info->driver_version, sizeof(info->driver_version), "%d", drv);
+  info->device_index = device;
+  info->compute_units = p.multiProcessorCount;
+  info->clock_khz = p.clockRate;
+  info->wavefront_size = p.warpSize;
+  info->global_mem_bytes = p.totalGlobalMem;
+  info->lds_bytes_per_block = p.sharedMemPerBlock;
+  info->host_unified_memory = p.integrated ? 1 : 0;
+  info->has_fp16 = 1;
+  return SULIMO_HIP_OK;
+}
+
+static int32_t create_ctx(int device, bool shared, sulimo_hip_ctx **out) {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return fail(SULIMO_HIP_ERR_DEVICE_NOT_FOUND, "no HIP device visible");
+  if (device < 0 || device >= count)
+    return fail(SULIMO_HIP_ERR_DEVICE_NOT_FOUND, "device index out of range");
+  sulimo_hip_ctx *c = new sulimo_hip_ctx();
+  c->device = device;
+  c->shared = shared;
+  int32_t rc = fill_info(device, &c->info);
+  if (rc) {
+    delete c;
+    return rc;
+  }
+  if (strncmp(c->info.arch_name, "gfx950", 6) != 0) {
+    std::string m = std::string("kernels are built for gfx950, device is ") + c->info.arch_name;
+    delete c;
+    return fail(SULIMO_HIP_ERR_BUILD_FAILED, m);
+  }
+  if ((e = hipSetDevice(device)) != hipSuccess || (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&c->done_event, hipEventBlockingSync | hipEventDisableTiming)) != hipSuccess ||
+      (e = hipEventCreate(&c->t0)) != hipSuccess || (e = hipEventCreate(&c->t1)) != hipSuccess) {
+    int32_t r = hip_fail(e, "context creation");
+    delete c;
+    return r;
+  }
+  *out = c;
+  return SULIMO_HIP_OK;
+}
+
+}  // namespace sulimo
+
+using namespace sulimo;
+
+extern "C" {
+
+const char *sulimo_hip_last_error(void) { return g_last_error.c_str(); }
+
+int32_t sulimo_hip_get_or_init(int32_t device, sulimo_hip_ctx **out) {
+  static std::mutex mu;
+  static sulimo_hip_ctx *shared[64] = {nullptr};
+  if (!out) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "out is null");
+  if (device < 0 || device >= 64) return fail(SULIMO_HIP_ERR_DEVICE_NOT_FOUND, "device index out of range");
+  std::lock_guard<std::mutex> g(mu);
+  if (!shared[device]) {
+    int32_t rc = create_ctx(device, true, &shared[device]);
+    if (rc) return rc;
+  }
+  *out = shared[device];
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_context_new(int32_t device, sulimo_hip_ctx **out) {
+  if (!out) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "out is null");
+  return create_ctx(device, false, out);
+}
+
+int32_t sulimo_hip_context_release(sulimo_hip_ctx *ctx) {
+  if (!ctx || ctx->shared) return SULIMO_HIP_OK;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  if (ctx->ws) hipFree(ctx->ws);
+  hipEventDestroy(ctx->done_event);
+  hipEventDestroy(ctx->t0);
+  hipEventDestroy(ctx->t1);
+  hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_finish(sulimo_hip_ctx *ctx) { return sulimo_hip_wait(ctx); }
+
+int32_t sulimo_hip_get_device_info(const sulimo_hip_ctx *ctx, sulimo_hip_device_info *out) {
+  if (!ctx || !out) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  *out = ctx->info;
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_probe(sulimo_hip_probe_result *out) {
+  if (!out) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "out is null");
+  memset(out, 0, sizeof(*out));
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0) {
+    snprintf(out->reason, sizeof(out->reason), "no HIP device: %s",
+             e == hipSuccess ? "device count is 0" : hipGetErrorString(e));
+    return SULIMO_HIP_OK;
+  }
+  for (int d = 0; d < count; d++) {
+    sulimo_hip_device_info info;
+    if (fill_info(d, &info) == SULIMO_HIP_OK && strncmp(info.arch_name, "gfx950", 6) == 0) {
+      out->available = 1;
+      out->info = info;
+      return SULIMO_HIP_OK;
+    }
+  }
+  snprintf(out->reason, sizeof(out->reason), "no gfx950 device among %d HIP devices", count);
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_wait(sulimo_hip_ctx *ctx) {
+  if (!ctx) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "ctx is null");
+  SULIMO_HIP_TRY(hipSetDevice(ctx->device));
+  SULIMO_HIP_TRY(hipEventRecord(ctx->done_event, ctx->stream));
+  hipError_t e = hipEventSynchronize(ctx->done_event);
+  if (e != hipSuccess) return hip_fail(e, "stream execution");
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "stream execution");
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_timer_start(sulimo_hip_ctx *ctx) {
+  if (!ctx) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "ctx is null");
+  SULIMO_HIP_TRY(hipEventRecord(ctx->t0, ctx->stream));
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_timer_stop(sulimo_hip_ctx *ctx, float *elapsed_ms) {
+  if (!ctx || !elapsed_ms) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  SULIMO_HIP_TRY(hipEventRecord(ctx->t1, ctx->stream));
+  SULIMO_HIP_TRY(hipEventSynchronize(ctx->t1));
+  SULIMO_HIP_TRY(hipEventElapsedTime(elapsed_ms, ctx->t0, ctx->t1));
+  return SULIMO_HIP_OK;
+}
+
+// ---- buffers ----
+
+int32_t sulimo_hip_buffer_create(sulimo_hip_ctx *ctx, void *host_ptr, size_t bytes,
+                                 int32_t read_only, sulimo_hip_buffer **out) {
+  if (!ctx || !out) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (bytes == 0) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "buffer size must be positive");
+  SULIMO_HIP_TRY(hipSetDevice(ctx->device));
+  void *dev = nullptr;
+  SULIMO_HIP_TRY(hipMalloc(&dev, bytes));
+  if (host_ptr) {
+    hipError_t e = hipMemcpyAsync(dev, host_ptr, bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+      hipFree(dev);
+      return hip_fail(e, "buffer upload");
+    }
+  }
+  sulimo_hip_buffer *b = new sulimo_hip_buffer();
+  b->dev = dev;
+  b->host = host_ptr;
+  b->bytes = bytes;
+  b->read_only = read_only != 0;
+  b->device = ctx->device;
+  g_active_buffers.fetch_add(1);
+  *out = b;
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_buffer_release(sulimo_hip_buffer *buf) {
+  if (!buf) return SULIMO_HIP_OK;
+  hipSetDevice(buf->device);
+  // hipFree waits for work that may still use the allocation.
+  hipError_t e = hipFree(buf->dev);
+  delete buf;
+  g_active_buffers.fetch_sub(1);
+  return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "buffer release");
+}
+
+size_t sulimo_hip_active_buffer_count(void) { return g_active_buffers.load(); }
+size_t sulimo_hip_buffer_size(const sulimo_hip_buffer *b) { return b ? b->bytes : 0; }
+void *sulimo_hip_buffer_device_ptr(const sulimo_hip_buffer *b) { return b ? b->dev : nullptr; }
+void *sulimo_hip_buffer_host_ptr(const sulimo_hip_buffer *b) { return b ? b->host : nullptr; }
+
+int32_t sulimo_hip_buffer_upload(sulimo_hip_ctx *ctx, sulimo_hip_buffer *buf, size_t offset,
+                                 size_t bytes, const void *src) {
+  if (!ctx || !buf || (!src && bytes)) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (offset > buf->bytes || bytes > buf->bytes - offset)
+    return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "upload range exceeds the buffer");
+  if (!bytes) return SULIMO_HIP_OK;
+  SULIMO_HIP_TRY(hipSetDevice(ctx->device));
+  // Pageable source: the copy is staged before the call returns, so `src` may be reused.
+  SULIMO_HIP_TRY(hipMemcpyAsync((char *)buf->dev + offset, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_buffer_download(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *buf,
+                                   size_t offset, size_t bytes, void *dst) {
+  if (!ctx || !buf || (!dst && bytes)) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (offset > buf->bytes || bytes > buf->bytes - offset)
+    return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "download range exceeds the buffer");
+  if (!bytes) return SULIMO_HIP_OK;
+  SULIMO_HIP_TRY(hipSetDevice(ctx->device));
+  SULIMO_HIP_TRY(hipMemcpyAsync(dst, (const char *)buf->dev + offset, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "download");
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_buffer_map_read(sulimo_hip_ctx *ctx, sulimo_hip_buffer *buf,
+                                   const void **mapped) {
+  if (!ctx || !buf || !mapped) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (!buf->host) return fail(SULIMO_HIP_ERR_ZERO_COPY, "buffer has no host mirror to map");
+  int32_t rc = sulimo_hip_buffer_download(ctx, buf, 0, buf->bytes, buf->host);
+  if (rc) return rc;
+  *mapped = buf->host;
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_buffer_unmap(sulimo_hip_ctx *ctx, sulimo_hip_buffer *buf, const void *mapped) {
+  if (!ctx || !buf) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  if (mapped && mapped != buf->host) return fail(SULIMO_HIP_ERR_ZERO_COPY, "pointer was not mapped from this buffer");
+  return SULIMO_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+"""Seeded random-init Q4_0 models and inputs of the shapes the benchmarks name.
+
+The weights are in the loader's Q4_0 SoA split (crates/sulimo-core/src/loader.rs:141-160,
+repack.rs:45-80): per tensor ``scales`` f16 [rows, cols/32] and ``quants`` u8
+[rows, cols/32, 16]. Distributions: nibbles uniform 0..15, d uniform in
+[0.002, 0.02] rounded to f16, norm weights 1 + N(0, 0.02) in f32, activations
+f16 N(0, 1), token ids uniform in [0, vocab). Every tensor draws from its own
+child stream of ``numpy.random.SeedSequence(seed)`` in declaration order.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    """The ModelConfig fields the prefill reads (crates/sulimo-core/src/model_config.rs:59-80)."""
+    n_layers: int
+    embd: int
+    ffn: int
+    n_head: int
+    n_head_kv: int
+    head_dim: int
+    rope_dim: int
+    vocab: int
+    rope_base: float
+    eps: float
+    rope_mode: int  # 0 = Norm (Llama), 1 = NeoX (Qwen2)
+
+    @property
+    def q_dim(self):
+        return self.n_head * self.head_dim
+
+    @property
+    def kv_dim(self):
+        return self.n_head_kv * self.head_dim
+
+    @property
+    def kv_bytes_per_pos(self):
+        return self.n_head_kv * (self.head_dim // 32) * 34
+
+
+# Qwen2.5-1.5B shape (28 layers, 1536 hidden, 12/2 heads, ffn 8960, vocab 151936, theta 1e6).
+QWEN25_1_5B = ModelConfig(28, 1536, 8960, 12, 2, 128, 128, 151936, 1e6, 1e-6, 1)
+# Llama-3.2-3B shape (28 layers, 3072 hidden, 24/8 heads, ffn 8192, vocab 128256, theta 5e5).
+LLAMA32_3B = ModelConfig(28, 3072, 8192, 24, 8, 128, 128, 128256, 5e5, 1e-5, 0)
+
+
+@dataclass
+class Q4Tensor:
+    scales: np.ndarray  # f16 [rows, cols/32]
+    quants: np.ndarray  # u8 [rows, cols/32, 16]
+
+    @property
+    def rows(self):
+        return self.scales.shape[0]
+
+    @property
+    def cols(self):
+        return self.scales.shape[1] * 32
+
+    def dequant_f32(self) -> np.ndarray:
+        """W[rows, cols] = (q - 8) * d (repack.rs:107-131 element order)."""
+        q = self.quants.astype(np.int16)
+        lo = (q & 15) - 8
+        hi = (q >> 4) - 8
+        w = np.concatenate([lo, hi], axis=-1).astype(np.float32)  # [rows, nb, 32]
+        w *= self.scales.astype(np.float32)[..., None]
+        return w.reshape(self.rows, self.cols)
+
+
+def random_q4(rng: np.random.Generator, rows: int, cols: int, d_lo=0.002, d_hi=0.02) -> Q4Tensor:
+    assert cols % 32 == 0
+    nb = cols // 32
+    scales = rng.uniform(d_lo, d_hi, size=(rows, nb)).astype(np.float16)
+    quants = np.frombuffer(rng.bytes(rows * nb * 16), dtype=np.uint8).reshape(rows, nb, 16).copy()
+    return Q4Tensor(scales, quants)
+
+
+@dataclass
+class HostLayer:
+    attn_norm: np.ndarray
+    q: Q4Tensor
+    k: Q4Tensor
+    v: Q4Tensor
+    o: Q4Tensor
+    ffn_norm: np.ndarray
+    gate: Q4Tensor
+    up: Q4Tensor
+    down: Q4Tensor
+
+
+@dataclass
+class HostModel:
+    cfg: ModelConfig
+    token_embd: Q4Tensor
+    output_norm: np.ndarray
+    output: Q4Tensor
+    layers: list = field(default_factory=list)
+
+
+def _norm(rng, n):
+    return (1.0 + rng.normal(0.0, 0.02, size=n)).astype(np.float32)
+
+
+def make_model(cfg: ModelConfig, seed: int, tie_embeddings: bool = True) -> HostModel:
+    """Random-init model. With tie_embeddings the LM head is token_embd (Qwen2.5
+    ties them; the engine falls back to token_embd when output.weight is absent,
+    crates/sulimo-engine/src/forward_pass.rs:58)."""
+    ss = np.random.SeedSequence(seed)
+    kids = iter(ss.spawn(4 + 9 * cfg.n_layers))
+    rng = lambda: np.random.default_rng(next(kids))  # noqa: E731
+    D, F = cfg.embd, cfg.ffn
+    token_embd = random_q4(rng(), cfg.vocab, D)
+    output_norm = _norm(rng(), D)
+    out_rng = rng()
+    output = token_embd if tie_embeddings else random_q4(out_rng, cfg.vocab, D)
+    layers = []
+    for _ in range(cfg.n_layers):
+        layers.append(HostLayer(
+            attn_norm=_norm(rng(), D), q=random_q4(rng(), cfg.q_dim, D), k=random_q4(rng(), cfg.kv_dim, D),
+            v=random_q4(rng(), cfg.kv_dim, D), o=random_q4(rng(), D, cfg.q_dim), ffn_norm=_norm(rng(), D),
+            gate=random_q4(rng(), F, D), up=random_q4(rng(), F, D), down=random_q4(rng(), D, F)))
+    return HostModel(cfg, token_embd, output_norm, output, layers)
+
+
+def random_tokens(seed: int, n: int, vocab: int) -> np.ndarray:
+    return np.random.default_rng(seed).integers(0, vocab, size=n, dtype=np.uint32)
+
+
+def random_activations(seed: int, shape) -> np.ndarray:
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float16)
+
+
+def embed_host(hm: HostModel, tokens: np.ndarray) -> np.ndarray:
+    """f16 token embeddings as lookup_token_embedding_f16 (scheduler.rs:329-374):
+    f16(d * (q - 8)) per element."""
+    t = hm.token_embd
+    rows = np.asarray(tokens, dtype=np.int64)
+    q = t.quants[rows].astype(np.int16)
+    w = np.concatenate([(q & 15) - 8, (q >> 4) - 8], axis=-1).astype(np.float32)
+    w *= t.scales[rows].astype(np.float32)[..., None]
+    return w.reshape(len(rows), hm.cfg.embd).astype(np.float16)

@@ -1,0 +1,37 @@
+"""Shared comparison helpers and deterministic fills for the parity tests."""
+import numpy as np
+
+
+def max_rel_err(got, ref) -> float:
+    """max |g - r| / max(|r|, 1): the reference's metric (crates/sulimo-ocl/tests/test_gemm.rs:45-57)."""
+    g = np.asarray(got, dtype=np.float64).ravel()
+    r = np.asarray(ref, dtype=np.float64).ravel()
+    return float(np.max(np.abs(g - r) / np.maximum(np.abs(r), 1.0))) if g.size else 0.0
+
+
+def cosine(a, b) -> float:
+    a = np.asarray(a, dtype=np.float64).ravel()
+    b = np.asarray(b, dtype=np.float64).ravel()
+    na, nb = np.linalg.norm(a), np.linalg.norm(b)
+    return float(a @ b / (na * nb)) if na > 0 and nb > 0 else 0.0
+
+
+def gemm_pattern_fill(m: int, k: int, n: int):
+    """Deterministic fills of crates/sulimo-ocl/tests/test_gemm.rs:110-127 (m outputs,
+    k inputs, n tokens): d = 0.05 + 0.01*(i%13), q = (3i)%16 | ((7i+1)%16) << 4,
+    x = ((i%19) - 9) * 0.1."""
+    nb = m * k // 32
+    i = np.arange(nb)
+    scales = (0.05 + 0.01 * (i % 13)).astype(np.float32).astype(np.float16).reshape(m, k // 32)
+    j = np.arange(nb * 16)
+    quants = (((3 * j) % 16) | ((((7 * j) + 1) % 16) << 4)).astype(np.uint8).reshape(m, k // 32, 16)
+    t = np.arange(n * k)
+    x = (((t % 19).astype(np.float32) - 9.0) * 0.1).astype(np.float16).reshape(n, k)
+    return scales, quants, x
+
+
+def prefill_act_fill(total: int) -> np.ndarray:
+    """Activation fill of crates/sulimo-ocl/tests/test_prefill.rs:83-89:
+    f16(5*sin(0.17 i) + ((i % 7) - 3))."""
+    i = np.arange(total, dtype=np.float32)
+    return (np.sin(i * np.float32(0.17)) * np.float32(5.0) + ((np.arange(total) % 7) - 3).astype(np.float32)).astype(np.float16)

@@ -1,0 +1,335 @@
+"""CPU tests that pin the oracle (oracle/oracle.c) against the reference's own
+known-answer tests, closed forms, invariants and independent float64
+implementations, so that a plausible mistake (dropped term, wrong sign or
+index, transposed operand, wrong rounding mode) fails one of them.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from sulimo_amd import synthetic as S
+from tests.helpers import gemm_pattern_fill, prefill_act_fill
+
+
+# ---- Q4_0 format (crates/sulimo-core/src/repack.rs) ----
+
+def test_repack_known_answer_bit_exact():
+    """repack.rs:137-179: 4 blocks, scale 0.5+0.25b, nibbles (i+b)%16 | ((2i+b)%16)<<4;
+    AoS and SoA dequantization agree bit for bit."""
+    aos = bytearray()
+    for b in range(4):
+        aos += np.float16(0.5 + b * 0.25).tobytes()
+        for i in range(16):
+            aos.append(((i + b) % 16) | (((i * 2 + b) % 16) << 4))
+    aos = np.frombuffer(bytes(aos), np.uint8)
+    sc, qu = oracle.repack_q4_0_aos_to_soa(aos)
+    a = oracle.dequant_q4_0_aos(aos)
+    s = oracle.dequant_q4_0_soa(sc, qu)
+    assert np.array_equal(a.view(np.uint32), s.view(np.uint32))
+    # closed form of block 1, element 3 (low nibble (3+1)%16 = 4) and element 19 (high (6+1)%16=7)
+    assert a[32 + 3] == (4 - 8) * 0.75 and a[32 + 19] == (7 - 8) * 0.75
+
+
+def test_repack_rejects_bad_lengths():
+    with pytest.raises(ValueError):
+        oracle.repack_q4_0_aos_to_soa(np.zeros(17, np.uint8))
+
+
+def test_q4_0_all_bytes_all_positions():
+    """Every byte value at every position of a block, several scales (incl. f16
+    subnormals): element i = (lo(q_i)-8)*d, element 16+i = (hi(q_i)-8)*d -- the GGUF
+    Q4_0 layout as ggml's dequantize_row_q4_0 documents it."""
+    scales = np.array([1.0, 0.013, 2.0 ** -20, 6.0e4], np.float16)
+    for d in scales:
+        for shift in range(16):
+            qs = np.roll(np.arange(256, dtype=np.uint8).reshape(16, 16), shift, axis=1)
+            sc = np.full(16, d, np.float16)
+            out = oracle.dequant_q4_0_soa(sc, qs).reshape(16, 32)
+            lo = (qs & 15).astype(np.float32) - 8
+            hi = (qs >> 4).astype(np.float32) - 8
+            want = np.concatenate([lo, hi], axis=1) * np.float32(d)
+            assert np.array_equal(out, want)
+
+
+# ---- Q8_0 (crates/sulimo-core/src/kv_cache.rs) ----
+
+def test_q8_0_known_answer_roundtrip():
+    """kv_cache.rs:215-234: 64 values 0.1i - 3.2 round-trip within 0.05."""
+    x = (np.arange(64, dtype=np.float32) * np.float32(0.1) - np.float32(3.2))
+    d = oracle.dequant_q8_0(oracle.quantize_f32_to_q8_0(x))
+    assert np.max(np.abs(d - x)) < 0.05
+
+
+def test_q8_0_special_cases():
+    # all-zero block: d = 0, codes 0
+    z = oracle.quantize_f32_to_q8_0(np.zeros(32, np.float32))
+    assert np.all(z == 0)
+    # amax 127 -> d = 1 exactly: .5 ties round away from zero (round, not rint)
+    x = np.concatenate([[127.0], np.arange(-15, 16) + 0.5]).astype(np.float32)
+    b = oracle.quantize_f32_to_q8_0(x)
+    assert b[:2].view(np.float16)[0] == 1.0
+    codes = b[2:].view(np.int8)
+    assert codes[0] == 127 and codes[1] == -15 and codes[16] == 1 and codes[15] == -1
+    # +-amax -> +-127
+    y = np.random.default_rng(0).standard_normal(32).astype(np.float32)
+    y[7] = -5.0
+    yc = oracle.quantize_f32_to_q8_0(y)[2:].view(np.int8)
+    assert yc[7] == -127
+    # scale stored as f16 with round-to-nearest-even, including f16 subnormals;
+    # numpy's float16 conversion is an independent implementation of IEEE binary16
+    for amax in [1.27e-4, 3.3e-6, 0.7, 1000.0, 65000.0]:
+        v = np.zeros(32, np.float32)
+        v[5] = amax
+        s = oracle.quantize_f32_to_q8_0(v)[:2].view(np.float16)[0]
+        assert s.view(np.uint16) == np.float16(np.float32(amax) / np.float32(127.0)).view(np.uint16)
+
+
+def test_q8_0_error_bound():
+    """Every value within half a step of its code: |x - q*d32| <= d32/2 with the f32 d."""
+    x = np.random.default_rng(1).standard_normal(32 * 50).astype(np.float32) * 3
+    b = oracle.quantize_f32_to_q8_0(x).reshape(-1, 34)
+    xb = x.reshape(-1, 32)
+    d32 = np.abs(xb).max(axis=1) / np.float32(127.0)
+    q = b[:, 2:].view(np.int8).astype(np.float32)
+    assert np.all(np.abs(xb - q * d32[:, None]) <= d32[:, None] * 0.5 + 1e-6)
+
+
+# ---- GEMM scalar reference (crates/sulimo-ocl/src/gemm.rs:106-147) ----
+
+def test_gemm_reference_vs_textbook():
+    """test_gemm.rs fills at (n=8, k=256, m=256) and random data vs float64 X @ W^T."""
+    for seed, (m, k, n) in enumerate([(256, 256, 8), (64, 512, 13)]):
+        if seed == 0:
+            sc, qu, x = gemm_pattern_fill(m, k, n)
+            w = S.Q4Tensor(sc, qu).dequant_f32()
+        else:
+            t = S.random_q4(np.random.default_rng(seed), m, k)
+            sc, qu, w = t.scales, t.quants, t.dequant_f32()
+            x = np.random.default_rng(seed + 9).standard_normal((n, k)).astype(np.float16)
+        y = oracle.gemm_q4_0_f16_scalar_reference(sc, qu, x, m, k, n).astype(np.float64)
+        ref = x.astype(np.float64) @ w.astype(np.float64).T
+        bound = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T * (k * 2.0 ** -24) \
+            + np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+        assert np.all(np.abs(y - ref) <= bound)
+
+
+def test_gemm_vectorized_equals_scalar_loop():
+    """The oracle's token-parallel restatement is bit-identical to a literal scalar loop
+    of gemm.rs:106-147 (same operation order) on a small case."""
+    t = S.random_q4(np.random.default_rng(3), 16, 64)
+    x = np.random.default_rng(4).standard_normal((3, 64)).astype(np.float16)
+    y = oracle.gemm_q4_0_f16_scalar_reference(t.scales, t.quants, x, 16, 64, 3)
+    nb = 2
+    for tok in range(3):
+        for r in range(16):
+            acc = np.float32(0)
+            for b in range(nb):
+                d = np.float32(t.scales[r, b])
+                bs = np.float32(0)
+                for i in range(16):
+                    q = int(t.quants[r, b, i])
+                    lo = np.float32((q & 15) - 8)
+                    hi = np.float32((q >> 4) - 8)
+                    bs = np.float32(bs + np.float32(np.float32(x[tok, 32 * b + i]) * lo + np.float32(x[tok, 32 * b + 16 + i]) * hi))
+                acc = np.float32(acc + np.float32(bs * d))
+            assert y[tok, r].view(np.uint16) == np.float16(acc).view(np.uint16)
+
+
+# ---- CPU kernels ----
+
+def test_vec_dot_q4_0_q8_0_avx2_vs_scalar():
+    """avx2.rs:352-396 pattern (8 blocks, scale 0.8+0.1b, byte v|(15-v)<<4 with v=(3i+b)%16,
+    activations sin(0.05 i)); rel err <= 1e-3, and the integer block sums are exact."""
+    aos = bytearray()
+    for b in range(8):
+        aos += np.float16(0.8 + b * 0.1).tobytes()
+        for i in range(16):
+            v = (i * 3 + b) % 16
+            aos.append(v | ((15 - v) << 4))
+    sc, qu = oracle.repack_q4_0_aos_to_soa(np.frombuffer(bytes(aos), np.uint8))
+    x = np.sin(np.arange(256, dtype=np.float32) * np.float32(0.05))
+    xq = oracle.quantize_f32_to_q8_0(x)
+    s = oracle.vec_dot_q4_0_q8_0(sc, qu, xq, 8, avx2=False)
+    a = oracle.vec_dot_q4_0_q8_0(sc, qu, xq, 8, avx2=True)
+    assert abs(s - a) / max(abs(s), 1e-5) <= 1e-3
+    # exact: sum_b d_w d_x * int_dot(w, x) in float64
+    w = S.Q4Tensor(sc.view(np.float16).reshape(1, 8), qu.reshape(1, 8, 16))
+    wq = np.round(w.dequant_f32().reshape(8, 32) / w.scales.astype(np.float32).reshape(8, 1))
+    xb = xq.reshape(8, 34)
+    xc = xb[:, 2:].view(np.int8).astype(np.float64)
+    dx = xb[:, :2].copy().view(np.float16).astype(np.float64).ravel()
+    exact = np.sum((wq * xc).sum(axis=1) * w.scales.astype(np.float64).ravel() * dx)
+    assert abs(a - exact) <= 1e-5 * abs(exact) + 1e-6
+
+
+def test_rmsnorm_unit_rms_and_avx2():
+    """scalar.rs:366-378: output of unit weights has RMS 1; AVX2 agrees with scalar."""
+    x = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    out = oracle.rmsnorm(x, np.ones(4, np.float32), 1e-5)
+    assert abs(np.sqrt(np.mean(out.astype(np.float64) ** 2)) - 1.0) < 1e-3
+    y = np.random.default_rng(2).standard_normal(1536).astype(np.float32)
+    w = (1 + np.random.default_rng(3).normal(0, 0.02, 1536)).astype(np.float32)
+    s, a = oracle.rmsnorm(y, w, 1e-6), oracle.rmsnorm(y, w, 1e-6, avx2=True)
+    ref = y.astype(np.float64) / np.sqrt(np.mean(y.astype(np.float64) ** 2) + 1e-6) * w
+    assert np.max(np.abs(s - ref)) < 1e-5 and np.max(np.abs(a - ref)) < 1e-5
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_rope_matches_complex_rotation(mode):
+    """rope_head_scalar as a complex multiplication (x_a + i x_b) * e^{i pos theta_j}:
+    Norm pairs (2j, 2j+1), NeoX pairs (j, j+d/2); pos 0 is the identity; norms are kept."""
+    d, base = 128, 1e6
+    v = np.random.default_rng(5).standard_normal(d).astype(np.float32)
+    assert np.array_equal(oracle.rope_head(v, 0, d, base, mode), v)
+    for pos in [1, 7, 1999]:
+        out = oracle.rope_head(v, pos, d, base, mode).astype(np.float64)
+        j = np.arange(d // 2)
+        a, b = (2 * j, 2 * j + 1) if mode == 0 else (j, j + d // 2)
+        theta = pos * np.power(float(base), -2.0 * j / d)
+        z = (v[a] + 1j * v[b]).astype(np.complex128) * np.exp(1j * theta)
+        tol = 2e-6 * pos + 1e-5
+        assert np.max(np.abs(out[a] - z.real)) < tol and np.max(np.abs(out[b] - z.imag)) < tol
+        assert abs(np.linalg.norm(out) - np.linalg.norm(v.astype(np.float64))) < 1e-4
+
+
+def test_softmax_and_swiglu():
+    s = oracle.softmax(np.array([1.0, 2.0, 3.0], np.float32))
+    assert abs(s.sum() - 1) < 1e-6 and s[2] > s[1] > s[0]
+    g = np.array([0.0, 1.0, -3.0, 20.0], np.float32)
+    u = np.array([5.0, 2.0, 1.0, 1.0], np.float32)
+    out = oracle.swiglu(g, u)
+    ref = g / (1 + np.exp(-g.astype(np.float64))) * u
+    assert out[0] == 0.0 and np.max(np.abs(out - ref)) < 1e-5
+
+
+def test_attention_vs_bruteforce():
+    """causal_gqa_decode_scalar (scalar.rs:287-359) vs float64 softmax(Q K^T / sqrt(d)) V over
+    dequantized Q8_0 rings, GQA mapping kv = h // (Hq/Hkv), sliding window on the ring."""
+    hq, hkv, hd, cap = 6, 2, 64, 16
+    rng = np.random.default_rng(8)
+    kr = oracle.quantize_f32_to_q8_0(rng.standard_normal((cap, hkv * hd)).astype(np.float32))
+    vr = oracle.quantize_f32_to_q8_0(rng.standard_normal((cap, hkv * hd)).astype(np.float32))
+    kd = oracle.dequant_q8_0(kr).reshape(cap, hkv, hd).astype(np.float64)
+    vd = oracle.dequant_q8_0(vr).reshape(cap, hkv, hd).astype(np.float64)
+    start, n = 10, 12
+    q = rng.standard_normal((n, hq, hd)).astype(np.float32)
+    out = oracle.attention_prefill_f32(q, kr, vr, start, cap, hq, hkv, hd, n).reshape(n, hq, hd)
+    for t in range(n):
+        P = start + t
+        keys = [p for p in range(max(0, P - cap + 1), P + 1)]
+        slots = [p % cap for p in keys]
+        for h in range(hq):
+            g = h // (hq // hkv)
+            sc = kd[slots, g] @ q[t, h].astype(np.float64) / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            p /= p.sum()
+            ref = p @ vd[slots, g]
+            assert np.max(np.abs(out[t, h] - ref)) < 1e-4
+
+
+def test_embedding_lookup_f16():
+    """lookup_token_embedding_f16 (scheduler.rs:329-374): f16(d * (q-8)) per element."""
+    t = S.random_q4(np.random.default_rng(6), 50, 256)
+    for tok in [0, 17, 49]:
+        e = oracle.lookup_token_embedding_f16(t.scales, t.quants, 256, tok)
+        want = t.dequant_f32()[tok].astype(np.float16)
+        assert np.array_equal(e.view(np.uint16), want.view(np.uint16))
+
+
+def test_kv_store_cl_matches_quantize():
+    """prefill.cl:72-116 restated == quantize_f32_to_q8_0 on the f16 values, ring slots
+    (start_pos + t) % capacity (test_prefill.rs:56-192 pattern)."""
+    n, bpb, cap, start = 16, 8, 64, 5
+    act = prefill_act_fill(n * bpb * 32).reshape(n, bpb * 32)
+    ring = oracle.cl_kv_store_q8_0(act, np.zeros(cap * bpb * 34, np.uint8), start, cap, bpb, n)
+    for t in range(n):
+        slot = (start + t) % cap
+        want = oracle.quantize_f32_to_q8_0(act[t].astype(np.float32))
+        assert np.array_equal(ring[slot * bpb * 34:(slot + 1) * bpb * 34], want)
+
+
+# ---- whole model ----
+
+def _textbook_prefill(hm, x16, n):
+    """Float64 textbook transformer with the device op order; K/V pass through the
+    oracle's Q8_0 codec (the cache format), everything else unrounded."""
+    c = hm.cfg
+    x = x16.astype(np.float64)
+    D, hd = c.embd, c.head_dim
+
+    def rms(v, w):
+        return v / np.sqrt(np.mean(v * v, axis=1, keepdims=True) + c.eps) * w
+
+    def rope(v, nh):
+        v = v.reshape(n, nh, hd).copy()
+        j = np.arange(c.rope_dim // 2)
+        a, b = (2 * j, 2 * j + 1) if c.rope_mode == 0 else (j, j + c.rope_dim // 2)
+        th = np.arange(n)[:, None] * np.power(float(c.rope_base), -2.0 * j / c.rope_dim)[None]
+        cs, sn = np.cos(th)[:, None], np.sin(th)[:, None]
+        va, vb = v[..., a].copy(), v[..., b].copy()
+        v[..., a], v[..., b] = va * cs - vb * sn, va * sn + vb * cs
+        return v.reshape(n, nh * hd)
+
+    for L in hm.layers:
+        h = rms(x, L.attn_norm)
+        q = rope(h @ L.q.dequant_f32().T.astype(np.float64), c.n_head)
+        k = rope(h @ L.k.dequant_f32().T.astype(np.float64), c.n_head_kv)
+        v = h @ L.v.dequant_f32().T.astype(np.float64)
+        k = oracle.dequant_q8_0(oracle.quantize_f32_to_q8_0(k.astype(np.float32))).reshape(n, -1)
+        v = oracle.dequant_q8_0(oracle.quantize_f32_to_q8_0(v.astype(np.float32))).reshape(n, -1)
+        ao = np.zeros((n, c.n_head * hd))
+        for hh in range(c.n_head):
+            g = hh // (c.n_head // c.n_head_kv)
+            s = q[:, hh * hd:(hh + 1) * hd] @ k[:, g * hd:(g + 1) * hd].T / np.sqrt(hd)
+            s = np.where(np.tril(np.ones((n, n), bool)), s, -np.inf)
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            p /= p.sum(axis=1, keepdims=True)
+            ao[:, hh * hd:(hh + 1) * hd] = p @ v[:, g * hd:(g + 1) * hd]
+        x = x + ao @ L.o.dequant_f32().T.astype(np.float64)
+        h = rms(x, L.ffn_norm)
+        gt = h @ L.gate.dequant_f32().T.astype(np.float64)
+        up = h @ L.up.dequant_f32().T.astype(np.float64)
+        x = x + (gt / (1 + np.exp(-gt)) * up) @ L.down.dequant_f32().T.astype(np.float64)
+    h = rms(x, hm.output_norm)
+    return h @ hm.output.dequant_f32().T.astype(np.float64)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_reference_vs_textbook(mode):
+    cfg = S.ModelConfig(2, 128, 256, 4, 2, 32, 32, 96, 10000.0, 1e-6, mode)
+    hm = S.make_model(cfg, 3)
+    toks = S.random_tokens(4, 12, cfg.vocab)
+    x = S.embed_host(hm, toks)
+    lg = oracle.prefill_reference(oracle.OracleModel(hm), oracle.OracleKv(cfg, 32), x, 0, all_logits=True)
+    ref = _textbook_prefill(hm, x, 12)
+    assert np.max(np.abs(lg - ref)) <= 2e-2 * np.abs(ref).max()
+    assert np.mean(np.argmax(lg, 1) == np.argmax(ref, 1)) >= 0.9
+
+
+def test_forward_token_vs_prefill_reference():
+    """forward_token (Q8_0 activations, AVX2 integer dots) tracks the fp16-activation
+    prefill: logits cosine >= 0.99 and equal argmax (test_prefill.rs:863-885 gates)."""
+    cfg = S.ModelConfig(2, 128, 256, 4, 2, 32, 32, 64, 10000.0, 1e-6, 1)
+    hm = S.make_model(cfg, 1)
+    om = oracle.OracleModel(hm)
+    toks = S.random_tokens(2, 16, cfg.vocab)
+    lg = oracle.prefill_reference(om, oracle.OracleKv(cfg, 64), S.embed_host(hm, toks), 0, all_logits=True)
+    kv = oracle.OracleKv(cfg, 64)
+    lt = np.stack([oracle.forward_token(om, kv, int(t), p) for p, t in enumerate(toks)])
+    cos = (lg * lt).sum(1) / np.linalg.norm(lg, axis=1) / np.linalg.norm(lt, axis=1)
+    assert cos.min() >= 0.99
+    assert np.argmax(lg[-1]) == np.argmax(lt[-1])
+
+
+def test_prefill_reference_chunked_equals_whole():
+    """Splitting a prompt into micro-batches (the engine's ubatch loop) leaves the
+    result unchanged when no chunk wraps the ring (attention sees the same keys)."""
+    cfg = S.ModelConfig(1, 128, 256, 4, 2, 32, 32, 64, 10000.0, 1e-6, 1)
+    hm = S.make_model(cfg, 9)
+    om = oracle.OracleModel(hm)
+    x = S.embed_host(hm, S.random_tokens(10, 20, cfg.vocab))
+    a = oracle.prefill_reference(om, oracle.OracleKv(cfg, 32), x, 0)
+    kv = oracle.OracleKv(cfg, 32)
+    oracle.prefill_reference(om, kv, x[:12], 0)
+    b = oracle.prefill_reference(om, kv, x[12:], 12)
+    assert np.array_equal(a, b)
