@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Prefill benchmark on one MI355X: tokens/s of a full 2048-token prefill of a
+random-init Qwen2.5-1.5B-shaped Q4_0 model (28 layers, hidden 1536, 12/2 heads,
+head_dim 128, FFN 8960, vocab 151936, Q8_0 KV ring of 2048 positions, last-token
+logits), plus the Q4_0 GEMM throughput at the one-layer M=512 shapes.
+
+One step = device embedding gather of the 2048 prompt ids + execute_prefill_ubatch
+(all 28 layers, final norm, LM head of the last token) ending in its blocking
+wait; weights, KV ring and scratch are resident in HBM before timing starts.
+
+Prints one JSON line. `roofline` is the Q4_0 GEMM kernel (the dominant kernel),
+with its per-launch GPU time taken from hipEvents recorded around every GEMM
+launch inside the timed steps. `cpu_baseline` times the CPU oracle's restatement
+of the reference forward_token (AVX2, one pinned core) on a bounded sample of
+the same prompt.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0
+SEED_MODEL = 0x5EED0002
+SEED_TOKENS = 0x5EED1002
+METRIC = "prefill tokens/s (Qwen2.5-1.5B Q4_0, 2048 tok)"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--ubatch", type=int, default=2048)
+    ap.add_argument("--cpu-sample", type=int, default=48, help="positions timed for the CPU baseline (0 = skip)")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the per-shape GEMM table")
+    return ap.parse_args()
+
+
+def traffic_from_profiles():
+    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary, if present."""
+    p = os.path.join(ROOT, "profiles", "gemm_q4_0_prefill2048_pmc.json")
+    if not os.path.exists(p):
+        return None
+    try:
+        with open(p) as f:
+            return float(json.load(f)["hbm_bytes_per_gemm_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def gemm_table(ctx, hip, S):
+    """TFLOP/s of each Q4_0 linear of one Qwen2.5-1.5B layer at M=512 and of the
+    up-projection at M=128, hipEvent-timed over 20 back-to-back launches."""
+    rng = np.random.default_rng(0x5EED0001)
+    shapes = [("q_proj", 512, 1536, 1536), ("k_proj", 512, 1536, 256), ("v_proj", 512, 1536, 256),
+              ("o_proj", 512, 1536, 1536), ("gate_proj", 512, 1536, 8960), ("up_proj", 512, 1536, 8960),
+              ("down_proj", 512, 8960, 1536), ("up_proj_m128", 128, 1536, 8960),
+              ("lm_head_m1", 1, 1536, 151936)]
+    out = {}
+    tot_flop, tot_ms = 0.0, 0.0
+    for name, M, K, N in shapes:
+        w = S.random_q4(rng, N, K)
+        x = rng.standard_normal((M, K)).astype(np.float16)
+        bufs = [hip.HipBuffer.from_host(ctx, w.scales, True), hip.HipBuffer.from_host(ctx, w.quants, True),
+                hip.HipBuffer.from_host(ctx, x, True), hip.HipBuffer.device_only(ctx, M * N * 2)]
+        for _ in range(3):
+            hip.enqueue_gemm_q4_0_f16(ctx, *bufs, N, K, M)
+        ctx.wait()
+        it = 20
+        ctx.timer_start()
+        for _ in range(it):
+            hip.enqueue_gemm_q4_0_f16(ctx, *bufs, N, K, M)
+        ms = ctx.timer_stop() / it
+        flop = 2.0 * M * N * K
+        byts = N * K * 18 / 32 + 2 * M * K + 2 * M * N
+        tf = flop / (ms * 1e-3) / 1e12
+        out[name] = {"M": M, "K": K, "N": N, "us": round(ms * 1e3, 2), "tflops": round(tf, 1),
+                     "frac_mfma_peak": round(tf / PEAK_F16_TFLOPS, 4),
+                     "gbs": round(byts / (ms * 1e-3) / 1e9, 1)}
+        if M == 512:
+            tot_flop += flop
+            tot_ms += ms
+        for b in bufs:
+            b.release()
+    out["layer_m512_total"] = {"us": round(tot_ms * 1e3, 2), "tflops": round(tot_flop / (tot_ms * 1e-3) / 1e12, 1),
+                               "frac_mfma_peak": round(tot_flop / (tot_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4)}
+    return out
+
+
+def cpu_baseline(hm, tokens, n_pos: int):
+    """forward_token (crates/sulimo-engine/src/forward_pass.rs:190-417) restated in the
+    oracle, on one pinned core: per-token time at n_pos evenly spaced positions of the
+    prompt with a pre-filled Q8_0 ring; tokens/s = 1 / mean per-token time."""
+    import oracle
+    cfg = hm.cfg
+    cpu = sorted(os.sched_getaffinity(0))[0]
+    os.sched_setaffinity(0, {cpu})
+    om = oracle.OracleModel(hm)
+    cap = len(tokens)
+    rng = np.random.default_rng(7)
+    ring = lambda: oracle.quantize_f32_to_q8_0(rng.standard_normal(cap * cfg.kv_dim).astype(np.float32))  # noqa: E731
+    kv = oracle.OracleKv(cfg, cap, k=[ring() for _ in range(cfg.n_layers)], v=[ring() for _ in range(cfg.n_layers)])
+    pos = [int(p) for p in np.linspace(0, cap - 1, n_pos).round()]
+    oracle.forward_token(om, kv, int(tokens[pos[0]]), pos[0])  # warm caches / page in weights
+    times = []
+    for p in pos:
+        t0 = time.perf_counter()
+        oracle.forward_token(om, kv, int(tokens[p]), p)
+        times.append(time.perf_counter() - t0)
+    mean = float(np.mean(times))
+    return {"value": round(1.0 / mean, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"forward_token (AVX2 Q4_0.Q8_0, per-token LM head) at {n_pos} evenly spaced positions "
+                      f"of the {cap}-token prompt on a pre-filled Q8_0 ring, 1 pinned core; "
+                      f"mean {mean * 1e3:.1f} ms/token, est. full prefill {mean * cap:.1f} s"}
+
+
+def main():
+    a = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only: the prefill path runs on a single MI355X "
+              f"(requested --gpus {a.gpus}, WORLD_SIZE {world}); multi-GPU runs are not part of this build.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from sulimo_amd import hip
+    from sulimo_amd import synthetic as S
+
+    cfg = S.QWEN25_1_5B
+    T = a.prompt
+    ctx = hip.HipContext.get_or_init(0)
+    hm = S.make_model(cfg, SEED_MODEL)
+    tokens = S.random_tokens(SEED_TOKENS, T, cfg.vocab)
+    dm = hip.DeviceModel(ctx, hm, capacity=T, max_n=min(a.ubatch, T))
+
+    def step():
+        pos = 0
+        while pos < T:
+            m = min(a.ubatch, T - pos)
+            dm.embed(tokens[pos:pos + m])
+            dm.execute_prefill_ubatch(pos, m)
+            pos += m
+
+    for _ in range(a.warmup):
+        step()
+    ctx.wait()
+
+    # Timed region: K steps with per-launch hipEvents on the context stream.
+    ctx.set_profiling(True)
+    ctx.wait()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    ctx.wait()
+    wall = time.perf_counter() - t0
+    st = ctx.prefill_stats()
+    ctx.set_profiling(False)
+
+    ms_per_step = wall / a.steps * 1e3
+    value = T * a.steps / wall
+
+    # Same steps without event records, for the overhead-free rate.
+    ctx.wait()
+    t1 = time.perf_counter()
+    for _ in range(a.steps):
+        step()
+    ctx.wait()
+    wall_np = time.perf_counter() - t1
+
+    g = st.gemm
+    gemm_ms = g.total_ms / max(g.launches, 1)
+    gemm_tf = g.flop / (g.total_ms * 1e-3) / 1e12 if g.total_ms > 0 else 0.0
+    traffic = traffic_from_profiles()
+    roofline = {"kernel": "gemm_q4_kernel (Q4_0 x f16 MFMA GEMM, all launches of a step)",
+                "bound": "mfma", "achieved": round(gemm_tf, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(gemm_tf / PEAK_F16_TFLOPS, 4), "traffic": traffic,
+                "launches_per_step": g.launches // max(a.steps, 1), "avg_launch_us": round(gemm_ms * 1e3, 2),
+                "flop_per_launch": g.flop / max(g.launches, 1)}
+
+    def cls(k):
+        return {"ms_per_step": round(k.total_ms / a.steps, 3), "launches_per_step": int(k.launches // a.steps),
+                "tflops": round(k.flop / (k.total_ms * 1e-3) / 1e12, 2) if k.total_ms > 0 and k.flop > 0 else None,
+                "gbs": round(k.bytes / (k.total_ms * 1e-3) / 1e9, 1) if k.total_ms > 0 else None}
+
+    extra = {"kernel_classes": {"gemm": cls(st.gemm), "attention": cls(st.attention), "norm": cls(st.norm),
+                                "rope_kv": cls(st.rope_kv)},
+             "value_without_event_records": round(T * a.steps / wall_np, 1),
+             "device": ctx.device_info.arch_name.decode()}
+    if not a.no_gemm:
+        extra["gemm_shapes"] = gemm_table(ctx, hip, S)
+    dm.release()
+
+    cpu = None
+    if a.cpu_sample > 0:
+        cpu = cpu_baseline(hm, tokens, a.cpu_sample)
+
+    line = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": a.steps,
+            "warmup": a.warmup, "ms_per_step": round(ms_per_step, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+            "data": "synthetic: random-init Qwen2.5-1.5B-shaped Q4_0 weights (nibbles uniform, d~U[0.002,0.02]), "
+                    "uniform token ids",
+            "config": {"workload": f"qwen2.5-1.5b-shaped q4_0 prefill, {T}-token prompt, batch 1, last-token logits",
+                       "layers": cfg.n_layers, "hidden": cfg.embd, "heads": f"{cfg.n_head}/{cfg.n_head_kv}",
+                       "ffn": cfg.ffn, "vocab": cfg.vocab, "kv_cache": f"q8_0 ring, capacity {T}",
+                       "ubatch": a.ubatch, "prompt_tokens": T},
+            "roofline": roofline, "cpu_baseline": cpu, "extra": extra}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -285,6 +285,29 @@ int32_t sulimo_hip_kv_sync_from_host(sulimo_hip_ctx *ctx, const sulimo_hip_kv_ca
                                      size_t start_pos, size_t n);
 
 /* ---- timing (the queue's CL_QUEUE_PROFILING_ENABLE, program.rs:145-153) ---- */
+/* Per kernel class GPU time of execute_prefill_ubatch launches, measured with
+ * hipEvents recorded around each launch on the context stream while profiling is
+ * on, plus the algorithmic work the launches performed. */
+typedef struct {
+  uint64_t launches;
+  double total_ms;
+  double flop;  /* algorithmic FLOPs (GEMM 2*m*n*k; attention 4*head_dim*sum of keys per head) */
+  double bytes; /* algorithmic HBM bytes (inputs read once + outputs written once) */
+} sulimo_hip_kernel_stat;
+
+typedef struct {
+  sulimo_hip_kernel_stat gemm;      /* Q4_0 x f16 GEMMs (QKV, O, gate/up, down, LM head) */
+  sulimo_hip_kernel_stat attention; /* causal GQA attention */
+  sulimo_hip_kernel_stat norm;      /* RMSNorm and residual conversion */
+  sulimo_hip_kernel_stat rope_kv;   /* RoPE + Q8_0 KV quantize/write + ring commit */
+  sulimo_hip_kernel_stat other;     /* embedding gather, argmax */
+  uint64_t prefill_calls;
+} sulimo_hip_prefill_stats;
+
+/* Turns per-launch event timing on or off and clears the statistics. */
+int32_t sulimo_hip_set_profiling(sulimo_hip_ctx *ctx, int32_t enable);
+int32_t sulimo_hip_get_prefill_stats(const sulimo_hip_ctx *ctx, sulimo_hip_prefill_stats *out);
+
 /* Record a start event on the context stream; stop records the end event, waits for
  * it and returns the elapsed GPU milliseconds between them. */
 int32_t sulimo_hip_timer_start(sulimo_hip_ctx *ctx);

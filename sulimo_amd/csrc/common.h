@@ -5,8 +5,18 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/sulimo_hip.h"
+
+// Kernel classes of the prefill statistics (sulimo_hip_prefill_stats fields).
+enum ProfClass : int { PROF_GEMM = 0, PROF_ATTN = 1, PROF_NORM = 2, PROF_ROPE_KV = 3, PROF_OTHER = 4 };
+
+struct ProfRecord {
+  int cls;
+  int ev;  // index into sulimo_hip_ctx::ev_pool
+  double flop, bytes;
+};
 
 // ---------------------------------------------------------------------------
 // Host-side objects behind the opaque C handles
@@ -22,6 +32,11 @@ struct sulimo_hip_ctx {
   // for ring-wrapping ubatches, per-row argmax partials.
   void *ws = nullptr;
   size_t ws_bytes = 0;
+  // Per-launch event timing (sulimo_hip_set_profiling).
+  bool prof = false;
+  std::vector<hipEvent_t> ev_pool;  // pairs: [2i] start, [2i+1] end
+  std::vector<ProfRecord> pending;
+  sulimo_hip_prefill_stats stats{};
 };
 
 struct sulimo_hip_buffer {
@@ -39,6 +54,12 @@ int32_t fail(int32_t code, const std::string &msg);
 int32_t hip_fail(hipError_t e, const char *what);
 // Grows ctx->ws to at least `bytes` (synchronizes the stream before freeing the old one).
 int32_t ensure_workspace(sulimo_hip_ctx *ctx, size_t bytes);
+// Event pair around one launch when profiling is on: prof_begin returns the pair
+// index (or -1), prof_end records the end event and queues the record;
+// prof_collect (after the stream drained) adds the elapsed times to ctx->stats.
+int prof_begin(sulimo_hip_ctx *ctx);
+void prof_end(sulimo_hip_ctx *ctx, int ev, int cls, double flop, double bytes);
+void prof_collect(sulimo_hip_ctx *ctx);
 
 #define SULIMO_HIP_TRY(call)                                   \
   do {                                                         \

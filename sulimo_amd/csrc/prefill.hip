@@ -6,6 +6,8 @@
 // enqueues anything, so a bad argument becomes SULIMO_HIP_ERR_INVALID_ARGUMENT
 // instead of an out-of-bounds device access.
 #include <limits.h>
+
+#include <algorithm>
 #include <stdio.h>
 #include <string.h>
 
@@ -71,6 +73,33 @@ int32_t gemm_plain(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
   a.seg[0] = GemmSegment{dp<const uint16_t>(scales), dp<const uint8_t>(quants), out, (int)m, (int)m, 0};
   a.nseg = 1;
   return launch_gemm_q4_0(a, ctx->stream);
+}
+
+// Runs one launch between profiling events (no-op events when profiling is off).
+template <typename F>
+int32_t timed(sulimo_hip_ctx *ctx, int cls, double flop, double bytes, F &&launch) {
+  const int ev = prof_begin(ctx);
+  const int32_t rc = launch();
+  prof_end(ctx, ev, cls, flop, bytes);
+  return rc;
+}
+
+// Algorithmic work of a GEMM launch: 2*m*n*k FLOPs; Q4_0 weights (18 bytes per 32),
+// activations and outputs moved once.
+double gemm_flop(const GemmArgs &g) {
+  double n = 0;
+  for (int i = 0; i < g.nseg; i++) n += g.seg[i].n;
+  if (g.epi == EPI_SWIGLU) n *= 2;
+  return 2.0 * g.m * n * g.k;
+}
+double gemm_bytes(const GemmArgs &g) {
+  double n = 0;
+  for (int i = 0; i < g.nseg; i++) n += g.seg[i].n;
+  const double wn = g.epi == EPI_SWIGLU ? 2 * n : n;
+  const double out = g.epi == EPI_F32 ? 4.0 * g.m * n
+                     : g.epi == EPI_RESID ? 8.0 * g.m * n  // f32 residual read + write
+                                          : 2.0 * g.m * n;
+  return wn * g.k * 18.0 / 32.0 + 2.0 * g.m * g.k + out;
 }
 
 }  // namespace
@@ -388,14 +417,16 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   hipStream_t s = ctx->stream;
   const int in = (int)n;
 
-  if ((rc = launch_f16_to_f32(dp<const uint16_t>(scratch->x), xres, n * D, s))) return rc;
+  if ((rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D, [&] { return launch_f16_to_f32(dp<const uint16_t>(scratch->x), xres, n * D, s); }))) return rc;
   for (size_t l = 0; l < L; l++) {
     const sulimo_hip_layer_tensors &T = tensors->layers[l];
     uint8_t *ring_k = dp<uint8_t>(kv->k_buffers[l]);
     uint8_t *ring_v = dp<uint8_t>(kv->v_buffers[l]);
     // 1. attention RMSNorm
-    if ((rc = launch_rmsnorm_f32(xres, dp<const float>(T.attn_norm), dp<uint16_t>(scratch->h), nullptr,
-                                 (int)D, cfg->eps, in, s)))
+    if ((rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
+           return launch_rmsnorm_f32(xres, dp<const float>(T.attn_norm), dp<uint16_t>(scratch->h), nullptr,
+                                     (int)D, cfg->eps, in, s);
+         })))
       return rc;
     // 2. q, k, v projections as one segmented GEMM
     GemmArgs g{};
@@ -408,13 +439,15 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     g.seg[1] = GemmSegment{dp<const uint16_t>(T.attn_k_scales), dp<const uint8_t>(T.attn_k_quants), scratch->k->dev, (int)kvd, (int)kvd, 0};
     g.seg[2] = GemmSegment{dp<const uint16_t>(T.attn_v_scales), dp<const uint8_t>(T.attn_v_quants), scratch->v->dev, (int)kvd, (int)kvd, 0};
     g.nseg = 3;
-    if ((rc = launch_gemm_q4_0(g, s))) return rc;
+    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(g), gemm_bytes(g), [&] { return launch_gemm_q4_0(g, s); }))) return rc;
     // 3-4. RoPE on q and k, Q8_0 of k and v into the ring (or staging when wrapping)
-    if ((rc = launch_rope_qkv_store(dp<uint16_t>(scratch->q), dp<const uint16_t>(scratch->k),
-                                    dp<const uint16_t>(scratch->v), (int)Hq, (int)Hkv, (int)hd,
-                                    cfg->rope_dim, cfg->rope_base, cfg->rope_mode, (int)start_pos, in,
-                                    staged ? stg_k : ring_k, staged ? stg_v : ring_v,
-                                    staged ? 0 : (int)(start_pos % cap), staged ? in : (int)cap, s)))
+    if ((rc = timed(ctx, PROF_ROPE_KV, 0, 2.0 * n * (qd + 2 * kvd) + 2.0 * n * qd + 2.0 * n * bpp, [&] {
+           return launch_rope_qkv_store(dp<uint16_t>(scratch->q), dp<const uint16_t>(scratch->k),
+                                        dp<const uint16_t>(scratch->v), (int)Hq, (int)Hkv, (int)hd,
+                                        cfg->rope_dim, cfg->rope_base, cfg->rope_mode, (int)start_pos, in,
+                                        staged ? stg_k : ring_k, staged ? stg_v : ring_v,
+                                        staged ? 0 : (int)(start_pos % cap), staged ? in : (int)cap, s);
+         })))
       return rc;
     // 5. causal GQA attention
     AttnArgs at{};
@@ -431,12 +464,18 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     at.n_head = (int)Hq;
     at.n_head_kv = (int)Hkv;
     at.head_dim = (int)hd;
-    if ((rc = launch_attention(at, s))) return rc;
+    double keys = 0;  // sum over queries of visible keys
+    for (size_t t = 0; t < n; t++) keys += (double)std::min(start_pos + t + 1, cap);
+    const double kv_read = 2.0 * (double)std::min(start_pos + n, cap) * bpp;
+    if ((rc = timed(ctx, PROF_ATTN, 4.0 * hd * Hq * keys, 4.0 * n * qd + kv_read, [&] { return launch_attention(at, s); }))) return rc;
     if (staged) {
       const size_t keep = std::min(n, cap);
       const size_t first = n - keep;
-      if ((rc = launch_ring_commit(stg_k + first * bpp, ring_k, bpp, (int)((start_pos + first) % cap), (int)cap, (int)keep, s))) return rc;
-      if ((rc = launch_ring_commit(stg_v + first * bpp, ring_v, bpp, (int)((start_pos + first) % cap), (int)cap, (int)keep, s))) return rc;
+      if ((rc = timed(ctx, PROF_ROPE_KV, 0, 4.0 * keep * bpp, [&] {
+             int32_t r = launch_ring_commit(stg_k + first * bpp, ring_k, bpp, (int)((start_pos + first) % cap), (int)cap, (int)keep, s);
+             return r ? r : launch_ring_commit(stg_v + first * bpp, ring_v, bpp, (int)((start_pos + first) % cap), (int)cap, (int)keep, s);
+           })))
+        return rc;
     }
     // 6-7. output projection, residual add fused: x += f16(Wo a)
     GemmArgs go{};
@@ -447,10 +486,12 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     go.epi = EPI_RESID;
     go.seg[0] = GemmSegment{dp<const uint16_t>(T.attn_out_scales), dp<const uint8_t>(T.attn_out_quants), xres, (int)D, (int)D, 0};
     go.nseg = 1;
-    if ((rc = launch_gemm_q4_0(go, s))) return rc;
+    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s); }))) return rc;
     // 8. FFN RMSNorm
-    if ((rc = launch_rmsnorm_f32(xres, dp<const float>(T.ffn_norm), dp<uint16_t>(scratch->h), nullptr,
-                                 (int)D, cfg->eps, in, s)))
+    if ((rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
+           return launch_rmsnorm_f32(xres, dp<const float>(T.ffn_norm), dp<uint16_t>(scratch->h), nullptr,
+                                     (int)D, cfg->eps, in, s);
+         })))
       return rc;
     // 9-10. gate and up projections with SwiGLU fused into the epilogue
     GemmArgs gu{};
@@ -463,7 +504,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     gu.nseg = 1;
     gu.scales_up = dp<const uint16_t>(T.ffn_up_scales);
     gu.quants_up = dp<const uint8_t>(T.ffn_up_quants);
-    if ((rc = launch_gemm_q4_0(gu, s))) return rc;
+    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gu), gemm_bytes(gu), [&] { return launch_gemm_q4_0(gu, s); }))) return rc;
     // 11-12. down projection, residual add fused
     GemmArgs gd{};
     gd.x = dp<const uint16_t>(scratch->ffn_swiglu);
@@ -473,15 +514,19 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     gd.epi = EPI_RESID;
     gd.seg[0] = GemmSegment{dp<const uint16_t>(T.ffn_down_scales), dp<const uint8_t>(T.ffn_down_quants), xres, (int)D, (int)D, 0};
     gd.nseg = 1;
-    if ((rc = launch_gemm_q4_0(gd, s))) return rc;
+    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s); }))) return rc;
   }
   // 13. output RMSNorm of all n rows (h), final residual back to scratch.x as f16
-  if ((rc = launch_rmsnorm_f32(xres, dp<const float>(tensors->output_norm), dp<uint16_t>(scratch->h),
-                               dp<uint16_t>(scratch->x), (int)D, cfg->eps, in, s)))
+  if ((rc = timed(ctx, PROF_NORM, 0, 8.0 * n * D + 4.0 * D, [&] {
+         return launch_rmsnorm_f32(xres, dp<const float>(tensors->output_norm), dp<uint16_t>(scratch->h),
+                                   dp<uint16_t>(scratch->x), (int)D, cfg->eps, in, s);
+       })))
     return rc;
   // 14. logits of the last token
   const char *hlast = reinterpret_cast<const char *>(scratch->h->dev) + (n - 1) * D * 2;
-  if ((rc = gemm_plain(ctx, tensors->output_scales, tensors->output_quants, hlast, scratch->logits->dev, V, D, 1, EPI_F32)))
+  if ((rc = timed(ctx, PROF_GEMM, 2.0 * V * D, V * D * 18.0 / 32.0 + 2.0 * D + 4.0 * V, [&] {
+         return gemm_plain(ctx, tensors->output_scales, tensors->output_quants, hlast, scratch->logits->dev, V, D, 1, EPI_F32);
+       })))
     return rc;
   // Optional per-position logits / top-1.
   if (outputs && (outputs->logits_all || outputs->argmax_all)) {
@@ -497,7 +542,12 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     }
   }
   // 15. one blocking wait for the whole ubatch
-  return sulimo_hip_wait(ctx);
+  rc = sulimo_hip_wait(ctx);
+  if (ctx->prof) {
+    prof_collect(ctx);
+    ctx->stats.prefill_calls++;
+  }
+  return rc;
 }
 
 int32_t sulimo_hip_execute_prefill_ubatch(sulimo_hip_ctx *ctx, const sulimo_hip_model_config *cfg,

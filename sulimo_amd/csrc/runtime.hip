@@ -47,6 +47,39 @@ int32_t ensure_workspace(sulimo_hip_ctx *ctx, size_t bytes) {
   return SULIMO_HIP_OK;
 }
 
+int prof_begin(sulimo_hip_ctx *ctx) {
+  if (!ctx->prof) return -1;
+  const int i = (int)ctx->pending.size();
+  while ((int)ctx->ev_pool.size() < 2 * (i + 1)) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return -1;
+    ctx->ev_pool.push_back(e);
+  }
+  if (hipEventRecord(ctx->ev_pool[2 * i], ctx->stream) != hipSuccess) return -1;
+  return i;
+}
+
+void prof_end(sulimo_hip_ctx *ctx, int ev, int cls, double flop, double bytes) {
+  if (ev < 0) return;
+  if (hipEventRecord(ctx->ev_pool[2 * ev + 1], ctx->stream) != hipSuccess) return;
+  ctx->pending.push_back(ProfRecord{cls, ev, flop, bytes});
+}
+
+void prof_collect(sulimo_hip_ctx *ctx) {
+  sulimo_hip_kernel_stat *st[5] = {&ctx->stats.gemm, &ctx->stats.attention, &ctx->stats.norm,
+                                   &ctx->stats.rope_kv, &ctx->stats.other};
+  for (const ProfRecord &r : ctx->pending) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, ctx->ev_pool[2 * r.ev], ctx->ev_pool[2 * r.ev + 1]) != hipSuccess) continue;
+    sulimo_hip_kernel_stat *k = st[r.cls];
+    k->launches++;
+    k->total_ms += ms;
+    k->flop += r.flop;
+    k->bytes += r.bytes;
+  }
+  ctx->pending.clear();
+}
+
 static int32_t fill_info(int device, sulimo_hip_device_info *info) {
   hipDeviceProp_t p;
   SULIMO_HIP_TRY(hipGetDeviceProperties(&p, device));
@@ -133,6 +166,7 @@ int32_t sulimo_hip_context_release(sulimo_hip_ctx *ctx) {
   hipEventDestroy(ctx->done_event);
   hipEventDestroy(ctx->t0);
   hipEventDestroy(ctx->t1);
+  for (hipEvent_t e : ctx->ev_pool) hipEventDestroy(e);
   hipStreamDestroy(ctx->stream);
   delete ctx;
   return SULIMO_HIP_OK;
@@ -176,6 +210,22 @@ int32_t sulimo_hip_wait(sulimo_hip_ctx *ctx) {
   if (e != hipSuccess) return hip_fail(e, "stream execution");
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "stream execution");
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_set_profiling(sulimo_hip_ctx *ctx, int32_t enable) {
+  if (!ctx) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "ctx is null");
+  int32_t rc = sulimo_hip_wait(ctx);
+  if (rc) return rc;
+  ctx->pending.clear();
+  ctx->stats = sulimo_hip_prefill_stats{};
+  ctx->prof = enable != 0;
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_get_prefill_stats(const sulimo_hip_ctx *ctx, sulimo_hip_prefill_stats *out) {
+  if (!ctx || !out) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "null argument");
+  *out = ctx->stats;
   return SULIMO_HIP_OK;
 }
 

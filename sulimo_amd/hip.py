@@ -123,6 +123,16 @@ class PrefillOutputsC(C.Structure):
     _fields_ = [("logits_all", _BP), ("argmax_all", _BP)]
 
 
+class KernelStat(C.Structure):
+    _fields_ = [("launches", C.c_uint64), ("total_ms", C.c_double), ("flop", C.c_double),
+                ("bytes", C.c_double)]
+
+
+class PrefillStats(C.Structure):
+    _fields_ = [("gemm", KernelStat), ("attention", KernelStat), ("norm", KernelStat),
+                ("rope_kv", KernelStat), ("other", KernelStat), ("prefill_calls", C.c_uint64)]
+
+
 def _declare(L):
     I32, SZ, P, F = C.c_int32, C.c_size_t, C.c_void_p, C.c_float
     sig = {
@@ -161,6 +171,8 @@ def _declare(L):
         "sulimo_hip_embed_tokens": (I32, [P, P, P, P, SZ, SZ, SZ, P]),
         "sulimo_hip_kv_sync_to_host": (I32, [P, C.POINTER(KvCacheC), SZ, SZ]),
         "sulimo_hip_kv_sync_from_host": (I32, [P, C.POINTER(KvCacheC), SZ, SZ]),
+        "sulimo_hip_set_profiling": (I32, [P, I32]),
+        "sulimo_hip_get_prefill_stats": (I32, [P, C.POINTER(PrefillStats)]),
         "sulimo_hip_timer_start": (I32, [P]),
         "sulimo_hip_timer_stop": (I32, [P, C.POINTER(C.c_float)]),
     }
@@ -223,6 +235,15 @@ class HipContext:
         i = DeviceInfo()
         _check(lib().sulimo_hip_get_device_info(self.handle, C.byref(i)))
         return i
+
+    def set_profiling(self, enable: bool):
+        """Per-launch hipEvent timing of execute_prefill_ubatch (clears the statistics)."""
+        _check(lib().sulimo_hip_set_profiling(self.handle, 1 if enable else 0))
+
+    def prefill_stats(self) -> PrefillStats:
+        st = PrefillStats()
+        _check(lib().sulimo_hip_get_prefill_stats(self.handle, C.byref(st)))
+        return st
 
     def timer_start(self):
         _check(lib().sulimo_hip_timer_start(self.handle))
