@@ -39,12 +39,26 @@ struct sulimo_hip_ctx {
   sulimo_hip_prefill_stats stats{};
 };
 
+// GEMM-layout copy of one Q4_0 matrix (or an interleaved gate/up pair), built from
+// the SoA buffers it is keyed on (q4_panels.hip).
+struct Q4Panels {
+  void *dev = nullptr;
+  size_t bytes = 0;
+  int n = 0, k = 0;
+  bool interleave = false;
+  uint64_t ids[4] = {0, 0, 0, 0};   // scales, quants, up scales, up quants
+  uint64_t vers[4] = {0, 0, 0, 0};  // their write versions when the copy was built
+};
+
 struct sulimo_hip_buffer {
   void *dev = nullptr;
   void *host = nullptr;  // host mirror (the reference's arena slice), may be null
   size_t bytes = 0;
   bool read_only = false;
   int device = 0;
+  uint64_t id = 0;       // unique per created buffer
+  uint64_t version = 0;  // bumped by every write through this library
+  std::vector<Q4Panels> panels;  // owned GEMM-layout copies (this buffer = their quants)
 };
 
 namespace sulimo {
@@ -81,9 +95,10 @@ enum GemmEpilogue : int {
 
 // One weight matrix of a (possibly segmented) GEMM: `n` output rows, its
 // scales/quants, and where its outputs go (column offset `col0` in out, row stride ldo).
+// One output segment of a GEMM: n output columns from a Q4_0 panel array (for
+// EPI_SWIGLU the interleaved gate/up panels of n output columns).
 struct GemmSegment {
-  const uint16_t *scales;
-  const uint8_t *quants;
+  const uint8_t *panels;
   void *out;
   int n;
   int ldo;
@@ -96,12 +111,28 @@ struct GemmArgs {
   int epi;
   GemmSegment seg[3];
   int nseg;
-  // EPI_SWIGLU: second weight matrix (up) with the same shape as seg[0] (gate).
-  const uint16_t *scales_up;
-  const uint8_t *quants_up;
+  // Tile grid, filled by the launcher: tiles_m x tiles_n tiles, visited in groups of
+  // group_m tile rows.
+  int tiles_m, tiles_n, group_m;
 };
 
 int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s);
+
+// Bytes of one panel record: 32 weight rows x one 64-wide k stage (1 KB quants + 128 B scales).
+constexpr int kQ4PanelRecord = 1152;
+
+// Panel copy (q4_panels.hip) of the n x k Q4_0 matrix (scales, quants), or of the
+// interleaved gate/up pair when up_scales is given; built on ctx's stream when
+// missing or stale. Buffer sizes are the caller's to check.
+int32_t get_q4_panels(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales, const sulimo_hip_buffer *quants,
+                      const sulimo_hip_buffer *up_scales, const sulimo_hip_buffer *up_quants, int n, int k,
+                      const uint8_t **out);
+size_t q4_panel_bytes(int n, int k, bool interleave);
+void release_q4_panels(sulimo_hip_buffer *b);
+// Marks a buffer as written (invalidates panel copies built from it).
+inline void wrote(const sulimo_hip_buffer *b) {
+  if (b) const_cast<sulimo_hip_buffer *>(b)->version++;
+}
 
 // Bandwidth kernels (prefill_ops.hip).
 int32_t launch_rmsnorm_f16(const uint16_t *x, const float *w, uint16_t *out, int d, float eps,

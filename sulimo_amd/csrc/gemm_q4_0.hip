@@ -5,25 +5,34 @@
 // crates/sulimo-core/src/repack.rs:107-131), f32 accumulation, epilogue per use.
 //
 // One workgroup = 4 wave64s; tile BM tokens x BN weight rows (BN = 4 waves x 32*FN).
-// k advances in stages of 64 (two Q4_0 blocks). The path is latency-bound unless
-// several stages are in flight, so:
-//  * X (activations) streams global -> LDS with global_load_lds_dwordx4 (no VGPR
-//    staging) into a ring of NS stage slots, NS-1 stages ahead of use. A slot is
-//    BM rows x 128 bytes with the 16-byte chunk c of row r stored at slot position
-//    c ^ ((r >> 1) & 7), which makes the MFMA A-fragment reads bank-conflict free.
-//  * Each wave streams the raw Q4_0 bytes of its own 32*FN weight rows (8 bytes per
-//    lane per block, plus the f16 scale) into registers PD stages ahead, and
-//    dequantizes them straight into MFMA B operands: (1024+q) - 1032 exactly, then
-//    * d (one rounding to f16). Every weight is dequantized once per workgroup and
-//    reused for all BM rows.
+// k advances in stages of 64 (two Q4_0 blocks).
+//  * Every operand streams global -> LDS with buffer_load ... lds (no VGPR staging)
+//    into a ring of NS stage slots, NS-1 stages ahead of use. Each lane's buffer
+//    offset is fixed for the whole kernel and the stage advances through the scalar
+//    offset, so a stage's DMA costs no vector instructions. Rows past the matrix
+//    get an offset past the buffer's end, which the buffer unit turns into zeros.
+//  * Weights come from the panel copy (q4_panels.hip): one stage of 32 rows is one
+//    1 KB run of quants plus 128 bytes of scales, fetched with full 16-byte lanes.
+//  * A slot holds the X tile (BM rows x 128 bytes, 16-byte chunk c of row r at slot
+//    position c ^ ((r >> 1) & 7): the MFMA A-fragment reads are bank-conflict free),
+//    the quants [BN rows][2 blocks][16 B] and the scales [BN rows][2 x f16].
+//  * Every ring slot is its own LDS variable and the stage loop is unrolled by NS, so
+//    the compiler can tell the refill of one slot from the reads of another and keeps
+//    the ring in flight instead of draining it before each read.
+//  * Each wave dequantizes its own 32*FN weight rows straight into MFMA B operands and
+//    reuses them for all BM rows: (1024+q) - 1032 exactly (low nibbles) or
+//    (1024+16q)/16 - 72 exactly (high nibbles), then * d with one rounding to f16.
 //  * v_mfma_f32_32x32x16_f16, lane layout: lane l supplies A[row l%32][k 8*(l/32)..+7]
 //    and B[k 8*(l/32)..+7][col l%32], and receives C[8*(r/4) + 4*(l/32) + r%4][l%32]
 //    in accumulator register r. MFMA step s of a stage covers stage k 16s..16s+15:
 //    block s/2, elements 16*(s%2) + 8*(l/32)..+7, i.e. the low (s even) or high
 //    (s odd) nibbles of bytes 8*(l/32)..+7 of the block.
-//  * One barrier per stage: wait for this stage's X slot (explicit vmcnt), barrier,
+//  * One barrier per stage: wait for this stage's slot (explicit vmcnt), barrier,
 //    then refill the slot every wave finished reading in the previous stage.
+//  * An odd block count ends in a half stage: its second block has scale 0 in the
+//    panels and its X chunks past K are zero-filled.
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 
@@ -34,35 +43,53 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) void glb_void;
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
-constexpr int kBK = 64;  // k per stage
+constexpr int kBK = 64;                   // k per stage
+constexpr uint32_t kOob = 0x80000000u;    // buffer offset past every buffer: reads as zero
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data format (gfx9)
+constexpr int kXcds = 8;                      // XCDs of an MI355X
 
 template <int J>
 using ic = std::integral_constant<int, J>;
 
-__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
-
-// Four nibbles packed one per byte (values 0..15) -> two half2 of (q-8)*d.
-__device__ __forceinline__ void dq4(uint32_t nib, half2v d2, half2v &a, half2v &b) {
-  const half2v off = {(_Float16)1032.0f, (_Float16)1032.0f};
-  // bytes [n0, 0x64, n1, 0x64] -> half2(1024+n0, 1024+n1), exact
-  const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, nib, 0x04010400u);
-  const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, nib, 0x04030402u);
-  a = (as_h2(p0) - off) * d2;
-  b = (as_h2(p1) - off) * d2;
+template <typename F, int... J>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, J...>) {
+  (f(ic<J>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// 8 bytes of one block row -> B operands of its low-nibble and high-nibble k-steps.
-__device__ __forceinline__ void dq8(uint2 q, uint32_t d, half8 &lo, half8 &hi) {
-  const half2v d2 = as_h2(d | (d << 16));
-  half2v l0, l1, l2, l3, h0, h1, h2, h3;
-  dq4(q.x & 0x0F0F0F0Fu, d2, l0, l1);
-  dq4(q.y & 0x0F0F0F0Fu, d2, l2, l3);
-  dq4((q.x >> 4) & 0x0F0F0F0Fu, d2, h0, h1);
-  dq4((q.y >> 4) & 0x0F0F0F0Fu, d2, h2, h3);
-  lo = half8{l0[0], l0[1], l1[0], l1[1], l2[0], l2[1], l3[0], l3[1]};
-  hi = half8{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, (int)kRsrcWord3);
+}
+
+// One buffer -> LDS DMA: active lane i writes 16 bytes at dst + 16*i.
+__device__ __forceinline__ void dma16(rsrc_t r, void *dst, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, (int)voff, soff, 0, 0);
+}
+
+// Four nibbles, one per byte in bits [3:0] (HI = false) or [7:4] (HI = true) with the
+// other bits clear -> two half2 of (q-8)*d.
+template <bool HI>
+__device__ __forceinline__ void dq4(uint32_t nib, half2v d2, half2v &a, half2v &b) {
+  // bytes [n0, 0x64, n1, 0x64] -> half2(1024 + n0, 1024 + n1), exact
+  const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, nib, 0x04010400u);
+  const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, nib, 0x04030402u);
+  if constexpr (HI) {  // 1024 + 16q: /16 - 72 = q - 8, one exact fma
+    const half2v s = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const half2v o = {(_Float16)-72.0f, (_Float16)-72.0f};
+    a = __builtin_elementwise_fma(as_h2(p0), s, o) * d2;
+    b = __builtin_elementwise_fma(as_h2(p1), s, o) * d2;
+  } else {
+    const half2v o = {(_Float16)1032.0f, (_Float16)1032.0f};
+    a = (as_h2(p0) - o) * d2;
+    b = (as_h2(p1) - o) * d2;
+  }
 }
 
 // s_waitcnt vmcnt(n) with expcnt and lgkmcnt left unconstrained (gfx9 encoding).
@@ -79,24 +106,42 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
   constexpr bool kSwiglu = (EPI == EPI_SWIGLU);
   constexpr int OUT_BN = kSwiglu ? BN / 2 : BN;   // output columns per tile
   constexpr int NX = FM;                          // X DMA instructions per wave per stage
-  constexpr int NQ = BN / 128;                    // quant DMA instructions per wave per stage
-  constexpr int NSC = BN / 128;                   // scale DMA instructions per wave per stage
-  constexpr int NDMA = NX + NQ + NSC;
-  // LDS slot layout: X tile | quants [BN rows][2 blocks][16 B] | scales [BN rows][2 dwords]
+  constexpr int NQ = FN;                          // quant DMA instructions per wave per stage
+  constexpr int NDMA = NX + NQ + 1;               // + one scale DMA per wave per stage
   constexpr int X_BYTES = BM * kBK * 2;
   constexpr int Q_BYTES = BN * 32;
-  constexpr int S_BYTES = BN * 8;
+  constexpr int S_BYTES = BN * 4;
   constexpr int SLOT = X_BYTES + Q_BYTES + S_BYTES;
   static_assert(!kSwiglu || FN % 2 == 0, "SwiGLU pairs gate and up fragments in one wave");
-  static_assert(BN % 128 == 0, "DMA split");
+  static_assert(kNS >= 2 && kNS <= 4, "ring depth");
 
-  __shared__ __attribute__((aligned(16))) char smem[kNS * SLOT];
+  __shared__ __attribute__((aligned(16))) char smem0[SLOT];
+  __shared__ __attribute__((aligned(16))) char smem1[SLOT];
+  __shared__ __attribute__((aligned(16))) char smem2[kNS > 2 ? SLOT : 16];
+  __shared__ __attribute__((aligned(16))) char smem3[kNS > 3 ? SLOT : 16];
+  auto slot_ptr = [&](auto J) -> char * {
+    constexpr int j = decltype(J)::value % kNS;
+    if constexpr (j == 0) return smem0;
+    else if constexpr (j == 1) return smem1;
+    else if constexpr (j == 2) return smem2;
+    else return smem3;
+  };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lg = lane >> 5;
 
+  // --- workgroup -> tile. Workgroups are dispatched round-robin over the XCDs, each with
+  // its own L2: XCD e runs a contiguous range of the tile order, and that order walks
+  // group_m tile rows at a time, so the workgroups resident on one XCD share their X
+  // rows and weight rows in its L2. Any XCD count gives the same tiles.
+  const int ntiles = a.tiles_m * a.tiles_n;
+  const int xcd = blockIdx.x % kXcds, jx = blockIdx.x / kXcds;
+  const int t = xcd * (ntiles / kXcds) + min(xcd, ntiles % kXcds) + jx;
+  const int grp = t / (a.group_m * a.tiles_n), tg = t - grp * a.group_m * a.tiles_n;
+  const int gm = min(a.group_m, a.tiles_m - grp * a.group_m);
+  const int tile_m = grp * a.group_m + tg % gm;
+  int tile_n = tg / gm;
   // --- tile -> (segment, first output column, first row) ---
-  int tile_n = blockIdx.x;
   int si = 0;
   for (; si < a.nseg - 1; si++) {
     const int tn = (a.seg[si].n + OUT_BN - 1) / OUT_BN;
@@ -105,96 +150,70 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
   }
   const GemmSegment seg = a.seg[si];
   const int c0 = tile_n * OUT_BN;
-  const int m0 = blockIdx.y * BM;
+  const int m0 = tile_m * BM;
   const int nb = a.k >> 5;           // Q4_0 blocks per weight row
-  const int nst = (nb + 1) >> 1;     // stages
-  const size_t nscale = (size_t)seg.n * nb;  // scales of one weight matrix
+  const int nst = (nb + 1) >> 1;     // stages (the last is a half stage when nb is odd)
 
-  // Logical tile row L -> (weight matrix, row). Wave w's fragment f covers rows
-  // w*32*FN + 32f .. +31; with SwiGLU its first FN/2 fragments are gate rows and the
-  // rest up rows of the same output columns.
-  auto map_row = [&](int L, const uint16_t *&sc, const uint8_t *&qu, bool &ok) -> int {
-    sc = seg.scales;
-    qu = seg.quants;
-    int col;
+  const int npanels = (seg.n + 31) / 32 * (kSwiglu ? 2 : 1);
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)a.m * (uint32_t)a.ldx * 2u);
+  const rsrc_t rp = make_rsrc(seg.panels, (uint32_t)npanels * (uint32_t)nst * (uint32_t)kQ4PanelRecord);
+
+  // Wave w's fragment f -> panel (or -1 past the matrix). Fragment f covers output
+  // columns c0 + 32*(FN*w + f) ..; with SwiGLU the wave covers 16*FN columns, its
+  // first FN/2 fragments are their gate panels and the rest the up panels.
+  auto panel_of = [&](int f) -> int {
+    int p;
     if constexpr (kSwiglu) {
-      const int w = L / (32 * FN), f = (L % (32 * FN)) / 32, r = L & 31;
-      const bool up = f >= FN / 2;
-      col = c0 + w * 16 * FN + 32 * (up ? f - FN / 2 : f) + r;
-      if (up) {
-        sc = a.scales_up;
-        qu = a.quants_up;
-      }
+      const int j = c0 / 32 + wave * (FN / 2) + (f % (FN / 2));
+      p = 2 * j + (f >= FN / 2 ? 1 : 0);
     } else {
-      col = c0 + L;
+      p = c0 / 32 + FN * wave + f;
     }
-    ok = col < seg.n;
-    return ok ? col : 0;
+    return p < npanels ? p : -1;
   };
 
-  // --- per-lane DMA sources ---
-  // X: wave instruction i covers tile rows 8*(FM*wave+i) .. +7, chunk c of row r lands at
+  // --- per-lane DMA offsets (bytes), fixed for the whole kernel ---
+  // X: wave instruction i covers tile rows 8*(FM*wave+i) .. +7; chunk c of row r lands at
   // slot position c ^ ((r >> 1) & 7).
-  const _Float16 *xsrc[NX];
-  int xhalf[NX];
+  uint32_t xoff[NX];
+  bool xhi[NX];  // chunk in the stage's second block
 #pragma unroll
   for (int i = 0; i < NX; i++) {
     const int row = 8 * (FM * wave + i) + (lane >> 3);
     const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-    int r = m0 + row;
-    if (r >= a.m) r = a.m - 1;
-    xsrc[i] = reinterpret_cast<const _Float16 *>(a.x) + (size_t)r * a.ldx + 8 * chunk;
-    xhalf[i] = chunk >> 2;
+    const int r = m0 + row;
+    xoff[i] = r < a.m ? ((uint32_t)r * (uint32_t)a.ldx + 8u * chunk) * 2u : kOob;
+    xhi[i] = chunk >= 4;
   }
-  // Quants: wave instruction i covers logical rows 32*(NQ*wave+i) + lane/2, block lane%2.
-  const uint8_t *qsrc[NQ];
+  // Quants: wave instruction f copies fragment f's 1 KB record run (lane = 16 bytes).
+  // Scales: lanes 8f .. 8f+7 of the wave's scale instruction copy fragment f's 128 bytes.
+  uint32_t qoff[NQ], soff;
 #pragma unroll
-  for (int i = 0; i < NQ; i++) {
-    const int L = 32 * (NQ * wave + i) + (lane >> 1);
-    const uint16_t *sc;
-    const uint8_t *qu;
-    bool ok;
-    const int row = map_row(L, sc, qu, ok);
-    qsrc[i] = qu + ((size_t)row * nb + (lane & 1)) * 16;
+  for (int f = 0; f < NQ; f++) {
+    const int p = panel_of(f);
+    qoff[f] = p >= 0 ? (uint32_t)p * (uint32_t)nst * kQ4PanelRecord + 16u * lane : kOob;
   }
-  // Scales: the two scales of a stage start at e = row*nb + 2*st, which is odd when nb is
-  // odd; each row loads the two aligned dwords covering e .. e+1 (clamped to the array).
-  const uint16_t *ssrc[NSC];
-  int srow[NSC];
-#pragma unroll
-  for (int i = 0; i < NSC; i++) {
-    const int L = 32 * (NSC * wave + i) + (lane >> 1);
-    const uint16_t *sc;
-    const uint8_t *qu;
-    bool ok;
-    srow[i] = map_row(L, sc, qu, ok);
-    ssrc[i] = sc;
+  {
+    const int f = lane >> 3;  // lanes past 8*FN never issue
+    const int p = f < FN ? panel_of(f) : -1;
+    soff = p >= 0 ? (uint32_t)p * (uint32_t)nst * kQ4PanelRecord + 1024u + 16u * (lane & 7) : kOob;
   }
 
-  auto issue = [&](int st) {  // always NDMA instructions (stages past the end reload stage 0)
+  // Always NDMA instructions, so vmcnt counts stay exact (stages past the end reload
+  // stage 0). kCheck: the stage may be the half stage of an odd block count.
+  auto issue = [&](auto J, int st, auto kCheck) {
     const int sst = st < nst ? st : 0;
-    char *slot = smem + (st % kNS) * SLOT;
+    char *slot = slot_ptr(J);
+    bool half = false;
+    if constexpr (decltype(kCheck)::value) half = (2 * sst + 1 == nb);
 #pragma unroll
     for (int i = 0; i < NX; i++) {
-      // a chunk past K (odd block count) re-reads the stage's first block: its weights are 0
-      const int kc = sst * kBK - ((sst * 2 + xhalf[i] < nb) ? 0 : 32);
-      __builtin_amdgcn_global_load_lds((glb_void *)(xsrc[i] + kc),
-                                       (lds_void *)(slot + 8 * (FM * wave + i) * kBK * 2), 16, 0, 0);
+      const uint32_t off = (half && xhi[i]) ? kOob : xoff[i];
+      dma16(rx, slot + 8 * (FM * wave + i) * kBK * 2, off, sst * kBK * 2);
     }
 #pragma unroll
-    for (int i = 0; i < NQ; i++) {
-      const int blk = min(sst * 2 + (lane & 1), nb - 1) - (lane & 1);  // clamp the odd tail block
-      __builtin_amdgcn_global_load_lds((glb_void *)(qsrc[i] + (size_t)blk * 16),
-                                       (lds_void *)(slot + X_BYTES + 32 * (NQ * wave + i) * 32), 16, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < NSC; i++) {
-      const size_t e = (size_t)srow[i] * nb + 2 * sst;
-      size_t d = (e & ~(size_t)1) + 2 * (lane & 1);
-      if (d + 2 > nscale) d = nscale - 2;  // never past the array (the value is then unused)
-      __builtin_amdgcn_global_load_lds((glb_void *)(ssrc[i] + d),
-                                       (lds_void *)(slot + X_BYTES + Q_BYTES + 32 * (NSC * wave + i) * 8), 4, 0, 0);
-    }
+    for (int f = 0; f < NQ; f++) dma16(rp, slot + X_BYTES + (NQ * wave + f) * 1024, qoff[f], sst * kQ4PanelRecord);
+    if (lane < 8 * FN) dma16(rp, slot + X_BYTES + Q_BYTES + FN * wave * 128, soff, sst * kQ4PanelRecord);
   };
 
   floatx16 acc[FM][FN];
@@ -202,19 +221,6 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
   for (int i = 0; i < FM; i++)
 #pragma unroll
     for (int f = 0; f < FN; f++) acc[i][f] = floatx16{};
-
-  // Per-lane weight rows of this wave's fragments (validity and scale parity).
-  bool wok[FN];
-  int epar[FN];
-#pragma unroll
-  for (int f = 0; f < FN; f++) {
-    const uint16_t *sc;
-    const uint8_t *qu;
-    bool ok;
-    const int row = map_row(wave * 32 * FN + 32 * f + l32, sc, qu, ok);
-    wok[f] = ok;
-    epar[f] = (row * nb) & 1;
-  }
 
   auto read_a = [&](const _Float16 *xb, int s, half8 (&ao)[FM]) {
 #pragma unroll
@@ -232,11 +238,8 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
         acc[i][f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao[i], bo[f], acc[i][f], 0, 0, 0);
   };
 
-  // prologue: stages 0..NS-2 in flight
-#pragma unroll
-  for (int s = 0; s < kNS - 1; s++) issue(s);
-
-  for (int st = 0; st < nst; st++) {
+  // One stage in slot J. kCheck: the stage or the one it prefetches may be the half stage.
+  auto stage = [&](auto J, int st, auto kCheck) {
     __builtin_amdgcn_sched_barrier(0);
     // stage st was issued NS-1 stages ago, (NS-2)*NDMA DMA instructions after it
     wait_vmcnt<(kNS - 2) * NDMA>();
@@ -244,35 +247,35 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
     // reads were consumed by its MFMAs; a fenced barrier would drain every prefetch
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue(st + kNS - 1);  // refills the slot read in stage st-1
-    const char *slot = smem + (st % kNS) * SLOT;
+    issue(ic<decltype(J)::value + kNS - 1>{}, st + kNS - 1, kCheck);  // refills the slot of stage st-1
+    const char *slot = slot_ptr(J);
     const _Float16 *xb = reinterpret_cast<const _Float16 *>(slot);
-    // raw weights of this wave's fragments: 8 bytes per block, and the 4 scales around e
+    // raw weights of this wave's fragments: 8 bytes per block, and the stage's 2 scales
     uint2 q[FN][2];
-    uint32_t dsc[FN][2];
+    half2v d2[FN][2];
 #pragma unroll
     for (int f = 0; f < FN; f++) {
       const int L = wave * 32 * FN + 32 * f + l32;
 #pragma unroll
       for (int b = 0; b < 2; b++)
         q[f][b] = *reinterpret_cast<const uint2 *>(slot + X_BYTES + L * 32 + b * 16 + 8 * lg);
-      const uint2 w = *reinterpret_cast<const uint2 *>(slot + X_BYTES + Q_BYTES + L * 8);
-      const uint32_t d0 = epar[f] ? (w.x >> 16) : (w.x & 0xffff);
-      const uint32_t d1 = epar[f] ? (w.y & 0xffff) : (w.x >> 16);
-      dsc[f][0] = (wok[f] && st * 2 < nb) ? d0 : 0u;
-      dsc[f][1] = (wok[f] && st * 2 + 1 < nb) ? d1 : 0u;
+      const uint32_t w = *reinterpret_cast<const uint32_t *>(slot + X_BYTES + Q_BYTES + L * 4);
+      d2[f][0] = as_h2(__builtin_amdgcn_perm(w, w, 0x01000100u));
+      d2[f][1] = as_h2(__builtin_amdgcn_perm(w, w, 0x03020302u));
     }
     auto dequant_step = [&](int s, half8 (&bo)[FN]) {
       const int b = s >> 1;
 #pragma unroll
       for (int f = 0; f < FN; f++) {
-        const half2v d2 = as_h2(dsc[f][b] | (dsc[f][b] << 16));
         const uint2 qq = q[f][b];
-        const uint32_t x0 = (s & 1) ? (qq.x >> 4) & 0x0F0F0F0Fu : qq.x & 0x0F0F0F0Fu;
-        const uint32_t x1 = (s & 1) ? (qq.y >> 4) & 0x0F0F0F0Fu : qq.y & 0x0F0F0F0Fu;
         half2v p0, p1, p2, p3;
-        dq4(x0, d2, p0, p1);
-        dq4(x1, d2, p2, p3);
+        if (s & 1) {
+          dq4<true>(qq.x & 0xF0F0F0F0u, d2[f][b], p0, p1);
+          dq4<true>(qq.y & 0xF0F0F0F0u, d2[f][b], p2, p3);
+        } else {
+          dq4<false>(qq.x & 0x0F0F0F0Fu, d2[f][b], p0, p1);
+          dq4<false>(qq.y & 0x0F0F0F0Fu, d2[f][b], p2, p3);
+        }
         bo[f] = half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
       }
     };
@@ -290,18 +293,33 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
     dequant_step(3, b1);
     mfmas(a0, b0);
     mfmas(a1, b1);
-  }
+  };
+
+  // Main loop: straight-line bodies of NS stages (no branches between stages keeps the
+  // wait analysis per slot) over the stages whose prefetch target is a full stage.
+  using yes = std::true_type;
+  using no = std::false_type;
+  static_for<kNS - 1>([&](auto J) { issue(J, decltype(J)::value, yes{}); });
+  const int nfull = nb >> 1;
+  const int nsafe = (nb & 1) ? nfull - (kNS - 1) : nst;  // stages st < nsafe prefetch full stages
+  int st0 = 0;
+  for (; st0 + kNS <= nsafe; st0 += kNS)
+    static_for<kNS>([&](auto J) { stage(J, st0 + decltype(J)::value, no{}); });
+  // Tail: fewer than 2*NS stages, each checked.
+  static_for<2 * kNS - 1>([&](auto J) {
+    if (st0 + decltype(J)::value < nst) stage(J, st0 + decltype(J)::value, yes{});
+  });
   // no DMA may still be writing this workgroup's LDS when it exits
   wait_vmcnt<0>();
 
   // --- epilogue: acc register r of fragment (i, f) is C[8*(r/4) + 4*lg + r%4][l32] ---
 #pragma unroll
   for (int i = 0; i < FM; i++) {
+    if constexpr (kSwiglu) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
-      if (row >= a.m) continue;
-      if constexpr (kSwiglu) {
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (row >= a.m) continue;
 #pragma unroll
         for (int f = 0; f < FN / 2; f++) {
           const int col = c0 + wave * 16 * FN + 32 * f + l32;
@@ -310,21 +328,45 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
           const float silu = g / (1.0f + __expf(-g));
           reinterpret_cast<_Float16 *>(seg.out)[(size_t)row * seg.ldo + seg.col0 + col] = (_Float16)(silu * u);
         }
-      } else {
+      }
+    } else if constexpr (EPI == EPI_RESID) {
+      // x += f16(acc): all loads of the fragment row group first, then the stores
+      float old[16][FN];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+          const int col = c0 + wave * 32 * FN + 32 * f + l32;
+          old[r][f] = (row < a.m && col < seg.n)
+                          ? reinterpret_cast<const float *>(seg.out)[(size_t)row * seg.ldo + seg.col0 + col]
+                          : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+          const int col = c0 + wave * 32 * FN + 32 * f + l32;
+          if (row < a.m && col < seg.n)
+            reinterpret_cast<float *>(seg.out)[(size_t)row * seg.ldo + seg.col0 + col] =
+                old[r][f] + (float)(_Float16)acc[i][f][r];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (row >= a.m) continue;
 #pragma unroll
         for (int f = 0; f < FN; f++) {
           const int col = c0 + wave * 32 * FN + 32 * f + l32;
           if (col >= seg.n) continue;
           const size_t o = (size_t)row * seg.ldo + seg.col0 + col;
           const float v = acc[i][f][r];
-          if constexpr (EPI == EPI_F16) {
-            reinterpret_cast<_Float16 *>(seg.out)[o] = (_Float16)v;
-          } else if constexpr (EPI == EPI_F32) {
-            reinterpret_cast<float *>(seg.out)[o] = v;
-          } else {  // EPI_RESID: x += f16(acc)
-            float *xo = reinterpret_cast<float *>(seg.out) + o;
-            *xo = *xo + (float)(_Float16)v;
-          }
+          if constexpr (EPI == EPI_F16) reinterpret_cast<_Float16 *>(seg.out)[o] = (_Float16)v;
+          else reinterpret_cast<float *>(seg.out)[o] = v;
         }
       }
     }
@@ -332,14 +374,16 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
 }
 
 template <int FM, int FN, int NS = 3>
-int32_t launch_cfg(const GemmArgs &a, hipStream_t s) {
+int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   constexpr int BM = 32 * FM;
   constexpr int BN = 128 * FN;
+  GemmArgs a = args;
   const int out_bn = (a.epi == EPI_SWIGLU) ? BN / 2 : BN;
-  int tiles_n = 0;
-  for (int i = 0; i < a.nseg; i++) tiles_n += (a.seg[i].n + out_bn - 1) / out_bn;
-  const int tiles_m = (a.m + BM - 1) / BM;
-  const dim3 grid(tiles_n, tiles_m), block(256);
+  a.tiles_n = 0;
+  for (int i = 0; i < a.nseg; i++) a.tiles_n += (a.seg[i].n + out_bn - 1) / out_bn;
+  a.tiles_m = (a.m + BM - 1) / BM;
+  a.group_m = 4;
+  const dim3 grid(a.tiles_m * a.tiles_n), block(256);
   switch (a.epi) {
     case EPI_F16: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F16>), grid, block, 0, s, a); break;
     case EPI_F32: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F32>), grid, block, 0, s, a); break;
@@ -356,10 +400,18 @@ int32_t launch_cfg(const GemmArgs &a, hipStream_t s) {
 int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
   if (a.m <= 0) return SULIMO_HIP_OK;
   if (a.k <= 0 || a.k % 32 != 0) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM k must be a positive multiple of 32");
+  if (a.ldx < a.k) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM activation row stride below k");
   if (a.nseg < 1 || a.nseg > 3) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM needs 1..3 segments");
-  for (int i = 0; i < a.nseg; i++)  // even row counts keep the scale DMA dword-aligned and in bounds
-    if (a.seg[i].n <= 0 || a.seg[i].n % 2 != 0)
-      return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM segments need a positive, even number of rows");
+  // Buffer offsets are 32-bit and stay below 2^31 (larger offsets mark rows past the end).
+  const uint64_t lim = 1ull << 31;
+  if ((uint64_t)a.m * (uint64_t)a.ldx * 2u >= lim)
+    return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM activations exceed 2 GiB");
+  for (int i = 0; i < a.nseg; i++) {
+    if (a.seg[i].n <= 0 || !a.seg[i].panels)
+      return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM segments need rows and a panel array");
+    if (q4_panel_bytes(a.seg[i].n, a.k, a.epi == EPI_SWIGLU) >= lim)
+      return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM weight matrix exceeds 2 GiB");
+  }
   if (a.epi == EPI_SWIGLU && a.nseg != 1)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "SwiGLU GEMM takes one segment");
   // Tile choice: each weight is dequantized once per workgroup and used for BM rows.

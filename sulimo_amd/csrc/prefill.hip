@@ -61,16 +61,21 @@ struct TokenBuf {
 };
 thread_local TokenBuf g_tok;
 
+// Y[n][m] = X[n][k] W[m][k]^T for the Q4_0 matrix W = (scales, quants), through its
+// panel copy (built on first use).
 int32_t gemm_plain(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
                    const sulimo_hip_buffer *quants, const void *x, void *out, size_t m, size_t k,
                    size_t n, int epi) {
+  const uint8_t *pan = nullptr;
+  int32_t rc = get_q4_panels(ctx, scales, quants, nullptr, nullptr, (int)m, (int)k, &pan);
+  if (rc) return rc;
   GemmArgs a{};
   a.x = reinterpret_cast<const uint16_t *>(x);
   a.m = (int)n;
   a.k = (int)k;
   a.ldx = (int)k;
   a.epi = epi;
-  a.seg[0] = GemmSegment{dp<const uint16_t>(scales), dp<const uint8_t>(quants), out, (int)m, (int)m, 0};
+  a.seg[0] = GemmSegment{pan, out, (int)m, (int)m, 0};
   a.nseg = 1;
   return launch_gemm_q4_0(a, ctx->stream);
 }
@@ -120,6 +125,7 @@ int32_t sulimo_hip_enqueue_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_b
   NEED(x, n * k * 2, "x");
   NEED(out, n * m * 2, "out");
   if (n == 0) return SULIMO_HIP_OK;
+  wrote(out);
   return gemm_plain(ctx, scales, quants, x->dev, out->dev, m, k, n, EPI_F16);
 }
 
@@ -151,6 +157,7 @@ int32_t sulimo_hip_enqueue_rmsnorm(sulimo_hip_ctx *ctx, const sulimo_hip_buffer 
   NEED(x, n * d * 2, "x");
   NEED(w, d * 4, "w");
   NEED(out, n * d * 2, "out");
+  wrote(out);
   return launch_rmsnorm_f16(dp<const uint16_t>(x), dp<const float>(w), dp<uint16_t>(out), (int)d,
                             eps, (int)n, ctx->stream);
 }
@@ -164,6 +171,7 @@ int32_t sulimo_hip_enqueue_rope(sulimo_hip_ctx *ctx, sulimo_hip_buffer *vec, siz
   if (mode != 0 && mode != 1) return fail(kInval, "rope mode must be 0 (Norm) or 1 (NeoX)");
   if (!fits_int(head_count * head_dim) || !fits_int(start_pos + n)) return fail(kInval, "rope shape too large");
   NEED(vec, n * head_count * head_dim * 2, "vec");
+  wrote(vec);
   return launch_rope_f16(dp<uint16_t>(vec), (int)head_count, (int)head_dim, (int)rope_dim,
                          freq_base, mode, (int)start_pos, (int)n, ctx->stream);
 }
@@ -177,6 +185,7 @@ int32_t sulimo_hip_enqueue_kv_store(sulimo_hip_ctx *ctx, const sulimo_hip_buffer
   if (!fits_int(start_pos + n) || !fits_int(capacity)) return fail(kInval, "kv_store shape too large");
   NEED(act, n * blocks_per_pos * 32 * 2, "act");
   NEED(kv_cache, capacity * blocks_per_pos * 34, "kv_cache");
+  wrote(kv_cache);
   return launch_kv_store_q8_0(dp<const uint16_t>(act), dp<uint8_t>(kv_cache), (int)start_pos,
                               (int)capacity, (int)blocks_per_pos, (int)n, ctx->stream);
 }
@@ -210,6 +219,7 @@ int32_t sulimo_hip_enqueue_attention_prefill(sulimo_hip_ctx *ctx, const sulimo_h
   a.n_head = (int)head_count;
   a.n_head_kv = (int)head_count_kv;
   a.head_dim = (int)head_dim;
+  wrote(out);
   return launch_attention(a, ctx->stream);
 }
 
@@ -221,6 +231,7 @@ int32_t sulimo_hip_enqueue_silu_mul(sulimo_hip_ctx *ctx, const sulimo_hip_buffer
   NEED(gate, total_elements * 2, "gate");
   NEED(up, total_elements * 2, "up");
   NEED(out, total_elements * 2, "out");
+  wrote(out);
   return launch_silu_mul(dp<const uint16_t>(gate), dp<const uint16_t>(up), dp<uint16_t>(out),
                          total_elements, ctx->stream);
 }
@@ -231,6 +242,7 @@ int32_t sulimo_hip_enqueue_add(sulimo_hip_ctx *ctx, sulimo_hip_buffer *a,
   if (rc) return rc;
   NEED(a, total_elements * 2, "a");
   NEED(b, total_elements * 2, "b");
+  wrote(a);
   return launch_add_f16(dp<uint16_t>(a), dp<const uint16_t>(b), total_elements, ctx->stream);
 }
 
@@ -246,6 +258,7 @@ int32_t sulimo_hip_enqueue_logits_final(sulimo_hip_ctx *ctx, const sulimo_hip_bu
   NEED(scales, vocab_size * (embd_dim / 32) * 2, "scales");
   NEED(quants, vocab_size * (embd_dim / 32) * 16, "quants");
   NEED(logits, vocab_size * 4, "logits");
+  wrote(logits);
   const char *xrow = reinterpret_cast<const char *>(x_all->dev) + token_idx * embd_dim * 2;
   return gemm_plain(ctx, scales, quants, xrow, logits->dev, vocab_size, embd_dim, 1, EPI_F32);
 }
@@ -263,6 +276,7 @@ int32_t sulimo_hip_embed_tokens(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *em
   NEED(embd_scales, vocab * (embd / 32) * 2, "embd_scales");
   NEED(embd_quants, vocab * (embd / 32) * 16, "embd_quants");
   NEED(x, n * embd * 2, "x");
+  wrote(x);
   if (g_tok.bytes < n * 4 || g_tok.device != ctx->device) {
     if (g_tok.p) {
       SULIMO_HIP_TRY(hipStreamSynchronize(ctx->stream));
@@ -313,6 +327,7 @@ static int32_t kv_sync(sulimo_hip_ctx *ctx, const sulimo_hip_kv_cache *kv, size_
       sulimo_hip_buffer *b = which ? kv->v_buffers[l] : kv->k_buffers[l];
       NEED(b, cap * bpp, "kv layer");
       if (!b->host) return fail(SULIMO_HIP_ERR_ZERO_COPY, "kv buffer has no host mirror");
+      if (!to_host) wrote(b);
       for (int s = 0; s < ns; s++) {
         char *dev = (char *)b->dev + segs[s][0] * bpp;
         char *host = (char *)b->host + segs[s][0] * bpp;
@@ -417,6 +432,17 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   hipStream_t s = ctx->stream;
   const int in = (int)n;
 
+  for (sulimo_hip_buffer *b : {scratch->x, scratch->h, scratch->q, scratch->k, scratch->v, scratch->attn_out,
+                               scratch->ffn_swiglu, scratch->logits})
+    wrote(b);
+  for (size_t l = 0; l < L; l++) {
+    wrote(kv->k_buffers[l]);
+    wrote(kv->v_buffers[l]);
+  }
+  if (outputs) {
+    wrote(outputs->logits_all);
+    wrote(outputs->argmax_all);
+  }
   if ((rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D, [&] { return launch_f16_to_f32(dp<const uint16_t>(scratch->x), xres, n * D, s); }))) return rc;
   for (size_t l = 0; l < L; l++) {
     const sulimo_hip_layer_tensors &T = tensors->layers[l];
@@ -428,6 +454,16 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
                                      (int)D, cfg->eps, in, s);
          })))
       return rc;
+    // panel copies of this layer's weights (built on the first ubatch)
+    const uint8_t *pq, *pk, *pv, *po, *pgu, *pd;
+    if ((rc = get_q4_panels(ctx, T.attn_q_scales, T.attn_q_quants, nullptr, nullptr, (int)qd, (int)D, &pq)) ||
+        (rc = get_q4_panels(ctx, T.attn_k_scales, T.attn_k_quants, nullptr, nullptr, (int)kvd, (int)D, &pk)) ||
+        (rc = get_q4_panels(ctx, T.attn_v_scales, T.attn_v_quants, nullptr, nullptr, (int)kvd, (int)D, &pv)) ||
+        (rc = get_q4_panels(ctx, T.attn_out_scales, T.attn_out_quants, nullptr, nullptr, (int)D, (int)qd, &po)) ||
+        (rc = get_q4_panels(ctx, T.ffn_gate_scales, T.ffn_gate_quants, T.ffn_up_scales, T.ffn_up_quants, (int)F,
+                            (int)D, &pgu)) ||
+        (rc = get_q4_panels(ctx, T.ffn_down_scales, T.ffn_down_quants, nullptr, nullptr, (int)D, (int)F, &pd)))
+      return rc;
     // 2. q, k, v projections as one segmented GEMM
     GemmArgs g{};
     g.x = dp<const uint16_t>(scratch->h);
@@ -435,9 +471,9 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     g.k = (int)D;
     g.ldx = (int)D;
     g.epi = EPI_F16;
-    g.seg[0] = GemmSegment{dp<const uint16_t>(T.attn_q_scales), dp<const uint8_t>(T.attn_q_quants), scratch->q->dev, (int)qd, (int)qd, 0};
-    g.seg[1] = GemmSegment{dp<const uint16_t>(T.attn_k_scales), dp<const uint8_t>(T.attn_k_quants), scratch->k->dev, (int)kvd, (int)kvd, 0};
-    g.seg[2] = GemmSegment{dp<const uint16_t>(T.attn_v_scales), dp<const uint8_t>(T.attn_v_quants), scratch->v->dev, (int)kvd, (int)kvd, 0};
+    g.seg[0] = GemmSegment{pq, scratch->q->dev, (int)qd, (int)qd, 0};
+    g.seg[1] = GemmSegment{pk, scratch->k->dev, (int)kvd, (int)kvd, 0};
+    g.seg[2] = GemmSegment{pv, scratch->v->dev, (int)kvd, (int)kvd, 0};
     g.nseg = 3;
     if ((rc = timed(ctx, PROF_GEMM, gemm_flop(g), gemm_bytes(g), [&] { return launch_gemm_q4_0(g, s); }))) return rc;
     // 3-4. RoPE on q and k, Q8_0 of k and v into the ring (or staging when wrapping)
@@ -484,7 +520,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     go.k = (int)qd;
     go.ldx = (int)qd;
     go.epi = EPI_RESID;
-    go.seg[0] = GemmSegment{dp<const uint16_t>(T.attn_out_scales), dp<const uint8_t>(T.attn_out_quants), xres, (int)D, (int)D, 0};
+    go.seg[0] = GemmSegment{po, xres, (int)D, (int)D, 0};
     go.nseg = 1;
     if ((rc = timed(ctx, PROF_GEMM, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s); }))) return rc;
     // 8. FFN RMSNorm
@@ -500,10 +536,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     gu.k = (int)D;
     gu.ldx = (int)D;
     gu.epi = EPI_SWIGLU;
-    gu.seg[0] = GemmSegment{dp<const uint16_t>(T.ffn_gate_scales), dp<const uint8_t>(T.ffn_gate_quants), scratch->ffn_swiglu->dev, (int)F, (int)F, 0};
+    gu.seg[0] = GemmSegment{pgu, scratch->ffn_swiglu->dev, (int)F, (int)F, 0};
     gu.nseg = 1;
-    gu.scales_up = dp<const uint16_t>(T.ffn_up_scales);
-    gu.quants_up = dp<const uint8_t>(T.ffn_up_quants);
     if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gu), gemm_bytes(gu), [&] { return launch_gemm_q4_0(gu, s); }))) return rc;
     // 11-12. down projection, residual add fused
     GemmArgs gd{};
@@ -512,7 +546,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     gd.k = (int)F;
     gd.ldx = (int)F;
     gd.epi = EPI_RESID;
-    gd.seg[0] = GemmSegment{dp<const uint16_t>(T.ffn_down_scales), dp<const uint8_t>(T.ffn_down_quants), xres, (int)D, (int)D, 0};
+    gd.seg[0] = GemmSegment{pd, xres, (int)D, (int)D, 0};
     gd.nseg = 1;
     if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s); }))) return rc;
   }

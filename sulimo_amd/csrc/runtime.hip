@@ -14,6 +14,7 @@ namespace sulimo {
 
 static thread_local std::string g_last_error;
 static std::atomic<size_t> g_active_buffers{0};
+static std::atomic<uint64_t> g_next_buffer_id{1};
 
 int32_t fail(int32_t code, const std::string &msg) {
   g_last_error = msg;
@@ -266,6 +267,7 @@ int32_t sulimo_hip_buffer_create(sulimo_hip_ctx *ctx, void *host_ptr, size_t byt
   b->bytes = bytes;
   b->read_only = read_only != 0;
   b->device = ctx->device;
+  b->id = g_next_buffer_id.fetch_add(1);
   g_active_buffers.fetch_add(1);
   *out = b;
   return SULIMO_HIP_OK;
@@ -274,6 +276,7 @@ int32_t sulimo_hip_buffer_create(sulimo_hip_ctx *ctx, void *host_ptr, size_t byt
 int32_t sulimo_hip_buffer_release(sulimo_hip_buffer *buf) {
   if (!buf) return SULIMO_HIP_OK;
   hipSetDevice(buf->device);
+  release_q4_panels(buf);
   // hipFree waits for work that may still use the allocation.
   hipError_t e = hipFree(buf->dev);
   delete buf;
@@ -295,6 +298,7 @@ int32_t sulimo_hip_buffer_upload(sulimo_hip_ctx *ctx, sulimo_hip_buffer *buf, si
   SULIMO_HIP_TRY(hipSetDevice(ctx->device));
   // Pageable source: the copy is staged before the call returns, so `src` may be reused.
   SULIMO_HIP_TRY(hipMemcpyAsync((char *)buf->dev + offset, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  wrote(buf);
   return SULIMO_HIP_OK;
 }
 

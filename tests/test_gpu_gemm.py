@@ -105,6 +105,46 @@ def test_lm_head_shape(ctx, M):
     assert max_rel_err(y, ref) <= 1e-2
 
 
+@pytest.mark.parametrize("n_tok,k,m_out", [(8, 96, 40), (33, 800, 72), (130, 2080, 264)])
+def test_odd_block_counts_and_ragged_rows(ctx, n_tok, k, m_out):
+    """K = 32 * odd (the GEMM's last 64-wide k stage holds one block) and row counts
+    that do not fill the 32-row weight panels: against the oracle's scalar reference
+    with the f16-weight error model, and against fp32 within 1e-2."""
+    rng = np.random.default_rng(5000 + k + m_out)
+    w = S.random_q4(rng, m_out, k)
+    x = rng.standard_normal((n_tok, k)).astype(np.float16)
+    y = run_gemm(ctx, w.scales, w.quants, x, m_out, k, n_tok)
+    ref = oracle.gemm_q4_0_f16_scalar_reference(w.scales, w.quants, x, m_out, k, n_tok)
+    err = np.abs(y.astype(np.float64) - ref.astype(np.float64))
+    assert np.all(err <= f16_weight_bound(x, w.scales, w.quants, ref))
+    assert max_rel_err(y, x.astype(np.float32) @ w.dequant_f32().T) <= 1e-2
+
+
+def test_panel_copy_follows_uploads(ctx):
+    """The GEMM reads a panel copy of the weights built from the SoA buffers on first
+    use; overwriting the buffers must be seen by the next GEMM (bit-exact one-hot
+    readback before and after)."""
+    rng = np.random.default_rng(21)
+    m_out, k = 64, 128
+    w1, w2 = S.random_q4(rng, m_out, k), S.random_q4(rng, m_out, k)
+    sb = hip.HipBuffer.from_host(ctx, w1.scales, True)
+    qb = hip.HipBuffer.from_host(ctx, w1.quants, True)
+    xb = hip.HipBuffer.from_host(ctx, np.eye(k, dtype=np.float16), True)
+    ob = hip.HipBuffer.device_only(ctx, k * m_out * 2)
+    got = []
+    for w in (w1, w2):
+        sb.upload(w.scales)
+        qb.upload(w.quants)
+        hip.enqueue_gemm_q4_0_f16(ctx, sb, qb, xb, ob, m_out, k, k)
+        ctx.wait()
+        got.append(ob.download(np.float16, (k, m_out)))
+    for b in (sb, qb, xb, ob):
+        b.release()
+    for w, y in zip((w1, w2), got):
+        want = oracle.dequant_q4_0_soa(w.scales, w.quants).reshape(m_out, k).T.astype(np.float16)
+        assert np.array_equal(y.view(np.uint16), want.view(np.uint16))
+
+
 def test_timed_gemm_profile(ctx):
     """gemm_q4_0_f16 (gemm.rs:28-102): waited launch with a GPU-time profile."""
     scales, quants, x = gemm_pattern_fill(1024, 1024, 512)
