@@ -15,7 +15,8 @@
 //    1 KB run of quants plus 128 bytes of scales, fetched with full 16-byte lanes.
 //  * A slot holds the X tile (BM rows x 128 bytes, 16-byte chunk c of row r at slot
 //    position c ^ ((r >> 1) & 7): the MFMA A-fragment reads are bank-conflict free),
-//    the quants [BN rows][2 blocks][16 B] and the scales [BN rows][2 x f16].
+//    the quants (per 32-row fragment: lane l's 16 bytes at 16*l, one linear read) and
+//    the scales [BN rows][2 x f16].
 //  * Every ring slot is its own LDS variable and the stage loop is unrolled by NS, so
 //    the compiler can tell the refill of one slot from the reads of another and keeps
 //    the ring in flight instead of draining it before each read.
@@ -100,7 +101,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 template <int FM, int FN, int kNS, int EPI>
-__global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
   constexpr int BM = 32 * FM;
   constexpr int BN = 128 * FN;                    // weight rows per tile (4 waves)
   constexpr bool kSwiglu = (EPI == EPI_SWIGLU);
@@ -113,18 +114,22 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
   constexpr int S_BYTES = BN * 4;
   constexpr int SLOT = X_BYTES + Q_BYTES + S_BYTES;
   static_assert(!kSwiglu || FN % 2 == 0, "SwiGLU pairs gate and up fragments in one wave");
-  static_assert(kNS >= 2 && kNS <= 4, "ring depth");
+  static_assert(kNS >= 2 && kNS <= 6, "ring depth");
 
   __shared__ __attribute__((aligned(16))) char smem0[SLOT];
   __shared__ __attribute__((aligned(16))) char smem1[SLOT];
   __shared__ __attribute__((aligned(16))) char smem2[kNS > 2 ? SLOT : 16];
   __shared__ __attribute__((aligned(16))) char smem3[kNS > 3 ? SLOT : 16];
+  __shared__ __attribute__((aligned(16))) char smem4[kNS > 4 ? SLOT : 16];
+  __shared__ __attribute__((aligned(16))) char smem5[kNS > 5 ? SLOT : 16];
   auto slot_ptr = [&](auto J) -> char * {
     constexpr int j = decltype(J)::value % kNS;
     if constexpr (j == 0) return smem0;
     else if constexpr (j == 1) return smem1;
     else if constexpr (j == 2) return smem2;
-    else return smem3;
+    else if constexpr (j == 3) return smem3;
+    else if constexpr (j == 4) return smem4;
+    else return smem5;
   };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -256,9 +261,9 @@ __global__ __launch_bounds__(256) void gemm_q4_kernel(GemmArgs a) {
 #pragma unroll
     for (int f = 0; f < FN; f++) {
       const int L = wave * 32 * FN + 32 * f + l32;
-#pragma unroll
-      for (int b = 0; b < 2; b++)
-        q[f][b] = *reinterpret_cast<const uint2 *>(slot + X_BYTES + L * 32 + b * 16 + 8 * lg);
+      const uint4 qv = *reinterpret_cast<const uint4 *>(slot + X_BYTES + (FN * wave + f) * 1024 + 16 * lane);
+      q[f][0] = uint2{qv.x, qv.y};
+      q[f][1] = uint2{qv.z, qv.w};
       const uint32_t w = *reinterpret_cast<const uint32_t *>(slot + X_BYTES + Q_BYTES + L * 4);
       d2[f][0] = as_h2(__builtin_amdgcn_perm(w, w, 0x01000100u));
       d2[f][1] = as_h2(__builtin_amdgcn_perm(w, w, 0x03020302u));
@@ -395,6 +400,18 @@ int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "gemm_q4_kernel launch");
 }
 
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
+
 }  // namespace
 
 int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
@@ -414,10 +431,17 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
   }
   if (a.epi == EPI_SWIGLU && a.nseg != 1)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "SwiGLU GEMM takes one segment");
-  // Tile choice: each weight is dequantized once per workgroup and used for BM rows.
+  // Tile choice: each weight is dequantized once per workgroup and reused for BM rows,
+  // and two workgroups share a CU. 128 x 256 tiles move the fewest bytes per MAC but
+  // only pay off when they fill the GPU at least twice over; otherwise 64 x 256.
   if (a.m <= 32) return launch_cfg<1, 2>(a, s);   // 32 x 256
   if (a.m <= 64) return launch_cfg<2, 2>(a, s);   // 64 x 256
-  return launch_cfg<4, 2>(a, s);                  // 128 x 256
+  int tiles128 = 0;
+  const int out128 = a.epi == EPI_SWIGLU ? 128 : 256;
+  for (int i = 0; i < a.nseg; i++) tiles128 += (a.seg[i].n + out128 - 1) / out128;
+  tiles128 *= (a.m + 127) / 128;
+  if (tiles128 >= 4 * cu_count()) return launch_cfg<4, 2>(a, s);  // 128 x 256
+  return launch_cfg<2, 2>(a, s);                            // 64 x 256
 }
 
 }  // namespace sulimo

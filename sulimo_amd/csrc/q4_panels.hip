@@ -8,7 +8,9 @@
 //
 //   panel p = weight rows 32p .. 32p+31, stage st = blocks 2st, 2st+1 (64 k);
 //   record (p, st) = 1152 bytes at (p * nst + st) * 1152, nst = ceil(nb / 2):
-//     bytes [0, 1024): 16-byte chunk c = quants of row 32p + c/2, block 2st + c%2
+//     bytes [0, 1024): 16-byte chunk 32h + r = quant bytes 8h .. 8h+7 of block 2st and
+//       then of block 2st+1, both of row 32p + r (h = 0, 1: the two half-waves of the
+//       MFMA B operand), so lane l of a wave reads its 16 bytes at 16*l
 //     bytes [1024, 1152): row r's scales of blocks 2st, 2st+1 at 1024 + 4r
 //   Rows past the matrix and the missing block of an odd block count hold scale 0
 //   and quants 0 (weight exactly zero). Same 18 bytes per 32 weights as Q4_0.
@@ -50,9 +52,13 @@ __global__ __launch_bounds__(256) void pack_q4_panels_kernel(PackArgs a) {
   const int sp = a.interleave ? (p >> 1) : p;
   uint4 v = {0u, 0u, 0u, 0u};
   if (c < 64) {
-    const int row = 32 * sp + (c >> 1), blk = 2 * st + (c & 1);
-    if (row < a.n && blk < a.nb)
-      v = *reinterpret_cast<const uint4 *>(a.quants[m] + ((size_t)row * a.nb + blk) * 16);
+    const int row = 32 * sp + (c & 31), h = c >> 5;
+    if (row < a.n) {
+      const uint8_t *q = a.quants[m] + ((size_t)row * a.nb + 2 * st) * 16 + 8 * h;
+      const uint2 lo = *reinterpret_cast<const uint2 *>(q);
+      const uint2 hi = 2 * st + 1 < a.nb ? *reinterpret_cast<const uint2 *>(q + 16) : uint2{0u, 0u};
+      v = uint4{lo.x, lo.y, hi.x, hi.y};
+    }
   } else {
     uint32_t w[4];
     for (int i = 0; i < 4; i++) {  // rows 4j .. 4j+3 of the panel, two scales each
