@@ -16,6 +16,10 @@
  *   - Q4_0 weights are the loader's SoA split (crates/sulimo-core/src/loader.rs:141-160):
  *     scales f16[m * k/32], quants u8[m * k/32 * 16]; element i of a block is the low
  *     nibble of byte i, element i+16 its high nibble, weight = (q - 8) * d.
+ *     The first GEMM that reads a (scales, quants) pair builds a device copy in the
+ *     GEMM's own layout (the same 18 bytes per 32 weights), kept until the quants
+ *     buffer is released; a write through this library to either buffer (upload or
+ *     a kernel output) makes the next GEMM rebuild it.
  *   - Q8_0 KV ring per layer (crates/sulimo-core/src/kv_cache.rs:27-90):
  *     [capacity][kv_dim/32] blocks of 34 bytes (f16 scale + 32 int8 codes).
  *   - enqueue_* calls are asynchronous on the context's single in-order stream;
