@@ -8,17 +8,26 @@
 // max(0, P-capacity+1) .. P (each once, at ring slot p % capacity), which is the
 // reference's range whenever P < capacity.
 //
-// Flash formulation, one workgroup = 4 wave64s = (BQ query positions) x (HG query
-// heads of one KV head):
-//  * K/V tiles of 64 keys are dequantized once per workgroup into LDS as f16
-//    (K row-major, V transposed), shared by all HG heads of the GQA group.
-//  * Each wave owns RF fragments of 16 query rows (one head, 16 positions) and
-//    computes S^T = K Q^T with v_mfma_f32_16x16x32_f16 (K as the A operand, Q^T as
-//    B, held in registers), so each lane holds 4 consecutive keys of one query:
-//    the running max/sum of the online softmax are per-lane scalars.
-//  * P^T (f16) feeds O^T = V^T P^T directly as the B operand: lane group g holds
-//    keys {4g..4g+3, 16+4g..16+4g+3} of each 32-key step, and the V^T A operand
-//    is read from LDS with the same key order.
+// Two kernels per call:
+//  1. kv_window_kernel dequantizes every key position the ubatch can see, once,
+//     from the ring (or the staging of a wrapping ubatch) into f16: K row-major
+//     [kv head][position][head_dim], V transposed [kv head][head_dim][position] with
+//     the positions of each 16-key group stored in the order the P V^T MFMA reads
+//     them (kperm). Values are f16(code * d), as the ring holds them.
+//  2. flash_attn_kernel: one workgroup = 8 wave64s. Four of them cover HG query
+//     heads of one KV head x PB blocks of 32 positions over the first half of the
+//     visible key tiles, the other four the same queries over the second half (two
+//     waves per SIMD, half the serial chain); the halves merge (m, l, O) through LDS
+//     at the end. K and V^T tiles of 64 keys stream into each half's two LDS slots by
+//     buffer DMA and are shared by its four waves. Per wave:
+//       S^T = K Q^T   v_mfma_f32_32x32x16_f16, K (LDS) as A, Q^T (registers) as B:
+//                     lane l holds 16 keys of query l%32, so the online-softmax
+//                     max and sum are per-lane scalars (plus one swap with l^32);
+//       P = exp2(S c - m), c = log2(e)/sqrt(head_dim) folded into one fma;
+//       O^T += V^T P^T  V^T (LDS) as A, P^T straight from the S^T registers as B.
+//     The accumulator is rescaled only on tiles where some running max moved.
+//     Tiles that a wave cannot see are skipped; masks are applied only on the
+//     tiles that cross the causal diagonal or the window start.
 #include <algorithm>
 
 #include "common.h"
@@ -28,245 +37,374 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 constexpr int kKT = 64;  // keys per tile
+constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
-template <int HD, int RF>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a, int BQ, int HG, int n_qblk,
-                                                   int n_hgrp) {
-  constexpr int KLD = HD + 8;   // Ks pitch (halves)
-  constexpr int VLD = kKT + 8;  // Vt pitch (halves)
-  constexpr int KS = HD / 32;   // MFMA k-steps over head_dim
-  constexpr int DF = HD / 16;   // output fragments over head_dim
-  __shared__ __attribute__((aligned(16))) _Float16 Ks[kKT * KLD];
-  __shared__ __attribute__((aligned(16))) _Float16 Vt[HD * VLD];
+// Stored slot s of a 16-key group holds key kperm(s): slots 0-7 = keys {0-3, 8-11}
+// and slots 8-15 = keys {4-7, 12-15}, the keys that lane halves 0 and 1 of the
+// S^T accumulator hold (an involution).
+__device__ __forceinline__ int kperm(int s) { return (s & 4) ? ((s & 8) ? s : s + 4) : ((s & 8) ? s - 4 : s); }
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, (int)kRsrcWord3);
+}
+__device__ __forceinline__ void dma16(rsrc_t r, void *dst, uint32_t voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, (int)voff, soff, 0, 0);
+}
+// s_waitcnt vmcnt(n) with expcnt and lgkmcnt left unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void wait_vmcnt0() { wait_vmcnt<0>(); }
+
+struct Window {
+  long lo;    // absolute position of window index 0
+  int len;    // visible positions
+  int pad;    // len rounded up to the tile
+};
+
+Window window_of(const AttnArgs &a) {
+  Window w;
+  w.lo = std::max(0L, (long)a.start_pos - a.capacity + 1);
+  w.len = (int)((long)a.start_pos + a.n - w.lo);
+  w.pad = (w.len + kKT - 1) / kKT * kKT;
+  return w;
+}
+
+// ---------------------------------------------------------------------------
+// 1. Q8_0 window -> f16 K [kvh][pos][HD] and V^T [kvh][HD][pos]
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void kv_window_kernel(AttnArgs a, long wlo, int wlen, int wpad) {
+  constexpr int NB = HD / 32;
+  __shared__ _Float16 vt[kKT][HD + 2];
+  const int kvh = blockIdx.y, j0 = blockIdx.x * kKT;
+  const int cap = a.capacity;
+  const size_t bpp = (size_t)a.n_head_kv * NB * 34;
+  const size_t hoff = (size_t)kvh * NB * 34;
+  _Float16 *kwin = reinterpret_cast<_Float16 *>(a.window);
+  _Float16 *vwin = kwin + (size_t)a.n_head_kv * wpad * HD;
+
+  for (int job = threadIdx.x; job < kKT * NB; job += blockDim.x) {
+    const int jj = job / NB, b = job % NB;
+    const int j = j0 + jj;
+    const long p = wlo + j;
+    float dk = 0.0f, dv = 0.0f;
+    const uint16_t *bk = nullptr, *bv = nullptr;
+    if (j < wlen) {
+      const bool staged = p >= a.new_pos0;
+      const size_t off = staged ? (size_t)(p - a.new_pos0) * bpp : (size_t)(p % cap) * bpp;
+      bk = reinterpret_cast<const uint16_t *>((staged ? a.new_k : a.k_ring) + off + hoff + (size_t)b * 34);
+      bv = reinterpret_cast<const uint16_t *>((staged ? a.new_v : a.v_ring) + off + hoff + (size_t)b * 34);
+      dk = (float)__builtin_bit_cast(_Float16, bk[0]);
+      dv = (float)__builtin_bit_cast(_Float16, bv[0]);
+    }
+    _Float16 *kdst = kwin + ((size_t)kvh * wpad + j) * HD + 32 * b;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      half8 kv8, vv8;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint16_t wk = bk ? bk[1 + 4 * c + e] : 0, wv = bv ? bv[1 + 4 * c + e] : 0;
+        kv8[2 * e] = (_Float16)((float)(int8_t)(wk & 0xff) * dk);
+        kv8[2 * e + 1] = (_Float16)((float)(int8_t)(wk >> 8) * dk);
+        vv8[2 * e] = (_Float16)((float)(int8_t)(wv & 0xff) * dv);
+        vv8[2 * e + 1] = (_Float16)((float)(int8_t)(wv >> 8) * dv);
+      }
+      *reinterpret_cast<half8 *>(kdst + 8 * c) = kv8;
+#pragma unroll
+      for (int e = 0; e < 8; e++) vt[jj][32 * b + 8 * c + e] = vv8[e];
+    }
+  }
+  __syncthreads();
+  // V^T rows: chunk c (8 keys) of row h holds keys 16*(c/2) + kperm(8*(c%2) + e)
+  for (int job = threadIdx.x; job < HD * (kKT / 8); job += blockDim.x) {
+    const int h = job / (kKT / 8), c = job % (kKT / 8);
+    half8 v;
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = vt[16 * (c >> 1) + kperm(8 * (c & 1) + e)][h];
+    *reinterpret_cast<half8 *>(vwin + ((size_t)kvh * HD + h) * wpad + j0 + 8 * c) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. flash attention over the f16 window
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo, int wpad, int HG, int PB,
+                                                            int n_qblk, int n_hgrp) {
+  constexpr int KS = HD / 16;          // S^T k-steps over head_dim
+  constexpr int OT = HD / 32;          // O^T tiles over head_dim
+  constexpr int KCH = HD / 8;          // 16-byte chunks per K row
+  constexpr int KROW = HD * 2;         // bytes per K row
+  constexpr int K_BYTES = kKT * KROW;
+  constexpr int V_BYTES = HD * kKT * 2;
+  constexpr int RPI = 64 / KCH;        // K rows per DMA instruction
+  constexpr int NKI = kKT / RPI / 4;   // K DMA instructions per wave per tile
+  constexpr int NVI = HD / 8 / 4;      // V^T DMA instructions per wave per tile (8 rows each)
+  // two halves of 4 waves, each with a two-slot ring; every slot is its own variable
+  __shared__ __attribute__((aligned(16))) char ka0[K_BYTES], va0[V_BYTES], ka1[K_BYTES], va1[V_BYTES];
+  __shared__ __attribute__((aligned(16))) char kb0[K_BYTES], vb0[V_BYTES], kb1[K_BYTES], vb1[V_BYTES];
+  __shared__ __attribute__((aligned(16))) float comb[4 * 64 * 16];  // one O^T tile of the second half
+  __shared__ float cml[4 * 64 * 2];                                 // its running max and sum
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l16 = lane & 15, lg = lane >> 4;
+  const int half = wave >> 2, qw = wave & 3;
+  const int l32 = lane & 31, lg = lane >> 5;
 
-  // Heaviest query blocks first (causal work grows with the position).
+  // Heaviest position blocks first (causal work grows with the position).
   int bid = blockIdx.x;
   const int hgrp = bid % n_hgrp;
   bid /= n_hgrp;
   const int kvh = bid % a.n_head_kv;
   const int qblk = n_qblk - 1 - bid / a.n_head_kv;
   const int G = a.n_head / a.n_head_kv;
-  const int q0 = qblk * BQ;                      // first token of the block
-  const int h0 = kvh * G + hgrp * HG;            // first query head
-  const int cap = a.capacity;
-  const size_t bpp = (size_t)a.n_head_kv * (HD / 32) * 34;
-  const size_t hoff = (size_t)kvh * (HD / 32) * 34;
+  const int hj = qw % HG, pb = qw / HG;
+  const int h = kvh * G + hgrp * HG + hj;
+  const int tw0 = (qblk * PB + pb) * 32;    // first token of this wave
+  const int t = tw0 + l32;                  // this lane's query token
   const int qd = a.n_head * HD;
-  const float scale_log2 = 1.4426950408889634f / sqrtf((float)HD);
+  const int cap = a.capacity;
+  const float c = 1.4426950408889634f / sqrtf((float)HD);
 
-  // --- load Q fragments (B operand of S^T = K Q^T) ---
-  half8 qf[RF][KS];
-  int tq[RF], hq[RF];
-  long pq[RF];
+  // Q^T fragments (B operand): lane holds Q[t][h][16s + 8lg .. +7]
+  half8 qf[KS];
+  {
+    const bool ok = t < a.n;
+    const _Float16 *src = reinterpret_cast<const _Float16 *>(a.q) + (size_t)(ok ? t : 0) * qd + (size_t)h * HD + 8 * lg;
 #pragma unroll
-  for (int i = 0; i < RF; i++) {
-    const int f = wave + 4 * i;
-    const int pb = f / HG, hj = f % HG;
-    tq[i] = q0 + 16 * pb + l16;
-    hq[i] = h0 + hj;
-    pq[i] = (long)a.start_pos + tq[i];
-    const bool ok = tq[i] < a.n && 16 * pb < BQ;
-    const _Float16 *src = reinterpret_cast<const _Float16 *>(a.q) + (size_t)(ok ? tq[i] : 0) * qd +
-                          (size_t)hq[i] * HD + 8 * lg;
-#pragma unroll
-    for (int s = 0; s < KS; s++)
-      qf[i][s] = ok ? *reinterpret_cast<const half8 *>(src + 32 * s) : half8{0, 0, 0, 0, 0, 0, 0, 0};
-  }
-
-  floatx4 o[RF][DF];
-  float mrun[RF], lrun[RF];
-#pragma unroll
-  for (int i = 0; i < RF; i++) {
-    mrun[i] = -INFINITY;
-    lrun[i] = 0.0f;
-#pragma unroll
-    for (int d = 0; d < DF; d++) o[i][d] = floatx4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  // Key window of the whole block.
-  const int t_last = min(q0 + BQ, a.n) - 1;
-  const long p_min = (long)a.start_pos + q0, p_max = (long)a.start_pos + t_last;
-  const long k_lo = max(0L, p_min - cap + 1), k_hi = p_max + 1;  // [k_lo, k_hi)
-  const long kt_begin = (k_lo / kKT) * kKT;
-
-  for (long kb = kt_begin; kb < k_hi; kb += kKT) {
-    // --- dequantize K and V tiles into LDS: jobs = 64 keys x KS blocks x {K,V} ---
-    for (int job = tid; job < kKT * KS * 2; job += 256) {
-      const int isv = job / (kKT * KS);
-      const int rem = job % (kKT * KS);
-      const int key = rem / KS, b = rem % KS;
-      const long p = kb + key;
-      float d = 0.0f;
-      int8_t codes[32];
-      if (p >= k_lo && p < k_hi) {
-        const uint8_t *base = (p < a.new_pos0) ? (isv ? a.v_ring : a.k_ring) + (size_t)(p % cap) * bpp
-                                               : (isv ? a.new_v : a.new_k) + (size_t)(p - a.new_pos0) * bpp;
-        const uint16_t *blk = reinterpret_cast<const uint16_t *>(base + hoff + (size_t)b * 34);
-        d = (float)__builtin_bit_cast(_Float16, blk[0]);
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-          uint16_t w = blk[1 + j];
-          codes[2 * j] = (int8_t)(w & 0xff);
-          codes[2 * j + 1] = (int8_t)(w >> 8);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 32; j++) codes[j] = 0;
-      }
-      if (!isv) {
-        _Float16 *dst = &Ks[key * KLD + 32 * b];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          half8 v;
-#pragma unroll
-          for (int e = 0; e < 8; e++) v[e] = (_Float16)((float)codes[8 * c + e] * d);
-          *reinterpret_cast<half8 *>(dst + 8 * c) = v;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 32; e++) Vt[(32 * b + e) * VLD + key] = (_Float16)((float)codes[e] * d);
-      }
+    for (int s = 0; s < KS; s++) {  // rows past n read row 0 and are zeroed (no branch)
+      const half8 v = *reinterpret_cast<const half8 *>(src + 16 * s);
+      qf[s] = ok ? v : half8{0, 0, 0, 0, 0, 0, 0, 0};
     }
-    __syncthreads();
+  }
 
+  // Absolute positions: this wave's queries, and the whole workgroup's.
+  const int P = a.start_pos + t;  // positions fit in int (checked by the callers)
+  const int tw_last = min(tw0 + 31, a.n - 1);
+  const bool wave_live = tw0 < a.n;
+  const int Pw_min = a.start_pos + tw0, Pw_max = a.start_pos + tw_last;
+  const int tg0 = qblk * PB * 32, tg_last = min(tg0 + PB * 32, a.n) - 1;
+  const int Pg_min = a.start_pos + tg0, Pg_max = a.start_pos + tg_last;
+  // window indices j = p - wlo of the keys any query of the workgroup sees
+  const int jlo = max(0, Pg_min - cap + 1 - (int)wlo), jhi = Pg_max - (int)wlo;  // inclusive
+  const int tile0 = jlo / kKT, tile1 = jhi / kKT;                                 // inclusive
+  // the first half takes the first ceil(n/2) tiles, the second half the rest
+  const int nsteps = (tile1 - tile0 + 2) / 2;
+  const int tb = half ? tile0 + nsteps : tile0;
+  const int te = half ? tile1 : tile0 + nsteps - 1;  // te < tb: nothing for this half
+
+  // DMA sources (bytes): K rows and V^T rows of this kv head; the tile start goes in soffset.
+  const _Float16 *kwin = reinterpret_cast<const _Float16 *>(a.window);
+  const _Float16 *vwin = kwin + (size_t)a.n_head_kv * wpad * HD;
+  const rsrc_t rk = make_rsrc(kwin + (size_t)kvh * wpad * HD, (uint32_t)wpad * HD * 2);
+  const rsrc_t rv = make_rsrc(vwin + (size_t)kvh * HD * wpad, (uint32_t)HD * wpad * 2);
+  uint32_t koff[NKI], voff[NVI];
 #pragma unroll
-    for (int i = 0; i < RF; i++) {
-      // --- S^T[key][query] for 4 key fragments ---
-      floatx4 s[4];
+  for (int i = 0; i < NKI; i++) {
+    const int row = RPI * (NKI * qw + i) + lane / KCH;
+    const int ch = (lane % KCH) ^ (row % KCH);
+    koff[i] = (uint32_t)(row * HD + 8 * ch) * 2u;
+  }
 #pragma unroll
-      for (int kf = 0; kf < 4; kf++) {
-        s[kf] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < NVI; i++) {
+    const int hr = 8 * (NVI * qw + i) + lane / 8;
+    const int ch = (lane % 8) ^ ((hr >> 1) & 7);
+    voff[i] = (uint32_t)(hr * wpad + 8 * ch) * 2u;
+  }
+  // always issued (an idle half reloads a valid tile), so every wave waits the same way
+  auto issue = [&](char *sk, char *sv, int tile) __attribute__((always_inline)) {
+    const int kb = min(tile, tile1) * kKT;
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-          half8 ka = *reinterpret_cast<const half8 *>(&Ks[(16 * kf + l16) * KLD + 32 * ks + 8 * lg]);
-          s[kf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qf[i][ks], s[kf], 0, 0, 0);
+    for (int i = 0; i < NKI; i++) dma16(rk, sk + RPI * (NKI * qw + i) * KROW, koff[i], kb * HD * 2);
+#pragma unroll
+    for (int i = 0; i < NVI; i++) dma16(rv, sv + 8 * (NVI * qw + i) * kKT * 2, voff[i], kb * 2);
+  };
+
+  floatx16 o[OT];
+#pragma unroll
+  for (int i = 0; i < OT; i++) o[i] = floatx16{};
+  float mrun = -INFINITY, lrun = 0.0f;
+
+  auto compute = [&](const char *sk, const char *sv, int tile) __attribute__((always_inline)) {
+    const int p0 = (int)wlo + tile * kKT;  // absolute position of the tile's first key
+    if (tile > te || !wave_live || p0 > Pw_max || p0 + kKT - 1 <= Pw_min - cap) return;  // nothing visible
+    const bool full = p0 + kKT - 1 <= Pw_min && p0 > Pw_max - cap;
+    // two halves of 32 keys, each a full online-softmax step
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+      __builtin_amdgcn_sched_barrier(0);  // bounds the live ranges the scheduler may stretch
+      floatx16 st = floatx16{};
+      const int row = 32 * kt + l32;
+#pragma unroll
+      for (int s = 0; s < KS; s++) {
+        const int pos = (2 * s + lg) ^ (row % KCH);
+        const half8 kf = *reinterpret_cast<const half8 *>(sk + row * KROW + 16 * pos);
+        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
+      }
+      if (!full) {  // wave-uniform; the per-key test is a select
+        const int pk = p0 + 32 * kt + 4 * lg;  // key of register 0 of this lane
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int p = pk + 8 * (r >> 2) + (r & 3);
+          st[r] = (p > P || p <= P - cap) ? -INFINITY : st[r];
         }
       }
-      // --- mask + online softmax (lane = one query, 16 keys) ---
-      const long P = pq[i];
-      const bool qok = tq[i] < a.n;
       float mt = -INFINITY;
 #pragma unroll
-      for (int kf = 0; kf < 4; kf++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const long p = kb + 16 * kf + 4 * lg + r;
-          const bool ok = qok && p <= P && p > P - cap && p >= k_lo;
-          const float v = ok ? s[kf][r] * scale_log2 : -INFINITY;
-          s[kf][r] = v;
-          mt = fmaxf(mt, v);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      // A query that sees no key yet keeps m = -inf; msafe keeps exp2 finite so that
-      // every lane runs the same MFMA sequence (no divergence around MFMA).
-      const float mnew = fmaxf(mrun[i], mt);
+      const float mnew = fmaxf(mrun, mt * c);
+      // a query that sees no key yet keeps m = -inf; msafe keeps exp2 finite so that
+      // every lane runs the same MFMA sequence
       const float msafe = mnew == -INFINITY ? 0.0f : mnew;
-      const float alpha = exp2f(mrun[i] - msafe);
-      mrun[i] = mnew;
-      float lsum = 0.0f;
+      const float alpha = __builtin_amdgcn_exp2f(mrun - msafe);
+      mrun = mnew;
       half8 pb[2];
+      float lsum = 0.0f;
 #pragma unroll
-      for (int kf = 0; kf < 4; kf++)
+      for (int r = 0; r < 16; r++) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], c, -msafe));
+        lsum += e;
+        pb[r >> 3][r & 7] = (_Float16)e;
+      }
+      lrun = lrun * alpha + lsum;
+      __builtin_amdgcn_sched_barrier(0);
+      if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float e = exp2f(s[kf][r] - msafe);
-          lsum += e;
-          pb[kf >> 1][(kf & 1) * 4 + r] = (_Float16)e;
-        }
-      lrun[i] = lrun[i] * alpha + lsum;
+        for (int i = 0; i < OT; i++) o[i] *= alpha;
+      }
 #pragma unroll
-      for (int d = 0; d < DF; d++) o[i][d] *= alpha;
-      // --- O^T[d][query] += V^T P^T over two 32-key steps ---
+      for (int jh = 0; jh < 2; jh++) {
+        const int j = 2 * kt + jh;  // 16-key step of the tile
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-#pragma unroll
-        for (int d = 0; d < DF; d++) {
-          const _Float16 *vr = &Vt[(16 * d + l16) * VLD + 32 * j + 4 * lg];
-          half4 v0 = *reinterpret_cast<const half4 *>(vr);
-          half4 v1 = *reinterpret_cast<const half4 *>(vr + 16);
-          half8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-          o[i][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[j], o[i][d], 0, 0, 0);
+        for (int i = 0; i < OT; i++) {
+          const int hr = 32 * i + l32;
+          const int pos = (2 * j + lg) ^ ((hr >> 1) & 7);
+          const half8 vf = *reinterpret_cast<const half8 *>(sv + hr * (kKT * 2) + 16 * pos);
+          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[jh], o[i], 0, 0, 0);
         }
       }
     }
+  };
+
+  // Per step: wait for this half's tile, barrier (it landed for all waves, and every
+  // wave finished the previous step), prefetch the next tile into the other slot,
+  // compute. Both halves run the same number of steps and barriers.
+  auto run = [&](char *k0, char *v0, char *k1, char *v1) __attribute__((always_inline)) {
+    issue(k0, v0, tb);
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+      wait_vmcnt0();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(k1, v1, tb + s + 1);
+      compute(k0, v0, tb + s);
+      wait_vmcnt0();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(k0, v0, tb + s + 2);
+      compute(k1, v1, tb + s + 1);
+    }
+    if (s < nsteps) {
+      wait_vmcnt0();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      compute(k0, v0, tb + s);
+    }
+  };
+  if (half == 0) run(ka0, va0, ka1, va1);
+  else run(kb0, vb0, kb1, vb1);
+  wait_vmcnt0();  // no DMA may still be writing this workgroup's LDS
+  __syncthreads();
+
+  // --- the second half hands its (m, l, O^T) to the first, one O^T tile at a time ---
+  const int ci = (qw * 64 + lane);
+  if (half) {
+    cml[2 * ci] = mrun;
+    cml[2 * ci + 1] = lrun;
+  }
+  float a0 = 1.0f, a1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < OT; i++) {
+    if (half) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 4)
+        *reinterpret_cast<float4 *>(&comb[ci * 16 + r]) = float4{o[i][r], o[i][r + 1], o[i][r + 2], o[i][r + 3]};
+    }
+    __syncthreads();
+    if (!half) {
+      if (i == 0) {
+        const float m1 = cml[2 * ci], l1 = cml[2 * ci + 1];
+        const float mm = fmaxf(mrun, m1);
+        const float ms = mm == -INFINITY ? 0.0f : mm;
+        a0 = __builtin_amdgcn_exp2f(mrun - ms);
+        a1 = __builtin_amdgcn_exp2f(m1 - ms);
+        lrun = lrun * a0 + l1 * a1;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) o[i][r] = o[i][r] * a0 + comb[ci * 16 + r] * a1;
+    }
     __syncthreads();
   }
+  if (half) return;
 
-  // --- normalize and store: lane holds O[query][16d + 4*lg + r] ---
+  // --- normalize and store: lane holds O[t][32i + 8(r/4) + 4lg + r%4] ---
+  float l = lrun + __shfl_xor(lrun, 32, 64);
+  if (t >= a.n) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  _Float16 *dst = reinterpret_cast<_Float16 *>(a.out) + (size_t)t * qd + (size_t)h * HD;
 #pragma unroll
-  for (int i = 0; i < RF; i++) {
-    float l = lrun[i];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
-    const int f = wave + 4 * i;
-    if (tq[i] >= a.n || 16 * (f / HG) >= BQ) continue;
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    _Float16 *dst = reinterpret_cast<_Float16 *>(a.out) + (size_t)tq[i] * qd + (size_t)hq[i] * HD;
+  for (int i = 0; i < OT; i++)
 #pragma unroll
-    for (int d = 0; d < DF; d++) {
-      half4 v = {(_Float16)(o[i][d][0] * inv), (_Float16)(o[i][d][1] * inv),
-                 (_Float16)(o[i][d][2] * inv), (_Float16)(o[i][d][3] * inv)};
-      *reinterpret_cast<half4 *>(dst + 16 * d + 4 * lg) = v;
+    for (int g = 0; g < 4; g++) {
+      const half4 v = {(_Float16)(o[i][4 * g] * inv), (_Float16)(o[i][4 * g + 1] * inv),
+                       (_Float16)(o[i][4 * g + 2] * inv), (_Float16)(o[i][4 * g + 3] * inv)};
+      *reinterpret_cast<half4 *>(dst + 32 * i + 8 * g + 4 * lg) = v;
     }
-  }
-}
-
-struct AttnShape {
-  int bq, hg, rf;
-};
-
-// Picks (positions, heads, fragments per wave) with 4 * rf == (bq/16) * hg:
-// prefer the most K/V reuse that still gives about two workgroups per CU.
-AttnShape pick_shape(int n, int G, int n_head_kv) {
-  static const AttnShape cands[] = {{32, 6, 3}, {64, 3, 3}, {48, 4, 3}, {192, 1, 3}, {16, 12, 3},
-                                    {32, 4, 2}, {64, 2, 2}, {128, 1, 2}, {16, 8, 2},
-                                    {32, 2, 1}, {64, 1, 1}, {16, 4, 1}};
-  AttnShape best{0, 0, 0};
-  long best_score = -1;
-  for (const AttnShape &c : cands) {
-    if (G % c.hg != 0) continue;
-    long wgs = (long)((n + c.bq - 1) / c.bq) * n_head_kv * (G / c.hg);
-    // score: enough workgroups first (up to 512), then reuse (rf * hg).
-    long score = std::min(wgs, 512L) * 64 + c.rf * c.hg;
-    if (score > best_score) {
-      best_score = score;
-      best = c;
-    }
-  }
-  return best;
 }
 
 template <int HD>
 int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
-  const int G = a.n_head / a.n_head_kv;
-  AttnShape sh = pick_shape(a.n, G, a.n_head_kv);
-  if (sh.rf == 0) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "no attention tiling for this head grouping");
-  const int n_qblk = (a.n + sh.bq - 1) / sh.bq;
-  const int n_hgrp = G / sh.hg;
-  dim3 grid(n_qblk * a.n_head_kv * n_hgrp), block(256);
-  switch (sh.rf) {
-    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, block, 0, s, a, sh.bq, sh.hg, n_qblk, n_hgrp); break;
-    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, block, 0, s, a, sh.bq, sh.hg, n_qblk, n_hgrp); break;
-    default: hipLaunchKernelGGL((attn_kernel<HD, 3>), grid, block, 0, s, a, sh.bq, sh.hg, n_qblk, n_hgrp); break;
-  }
+  const Window w = window_of(a);
+  hipLaunchKernelGGL((kv_window_kernel<HD>), dim3(w.pad / kKT, a.n_head_kv), dim3(256), 0, s, a, w.lo, w.len,
+                     w.pad);
   hipError_t e = hipGetLastError();
-  return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "attn_kernel launch");
+  if (e != hipSuccess) return hip_fail(e, "kv_window_kernel launch");
+  // 4 query waves = HG heads of one KV group x PB blocks of 32 positions, twice (the
+  // two halves of the key range)
+  const int G = a.n_head / a.n_head_kv;
+  const int HG = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
+  const int PB = 4 / HG;
+  const int n_qblk = (a.n + 32 * PB - 1) / (32 * PB);
+  const int n_hgrp = G / HG;
+  hipLaunchKernelGGL((flash_attn_kernel<HD>), dim3(n_qblk * a.n_head_kv * n_hgrp), dim3(512), 0, s, a, w.lo, w.pad,
+                     HG, PB, n_qblk, n_hgrp);
+  e = hipGetLastError();
+  return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "flash_attn_kernel launch");
 }
 
 }  // namespace
+
+size_t attention_window_bytes(const AttnArgs &a) {
+  const Window w = window_of(a);
+  return 2 * (size_t)a.n_head_kv * w.pad * a.head_dim * 2;
+}
 
 int32_t launch_attention(const AttnArgs &a, hipStream_t s) {
   if (a.n <= 0) return SULIMO_HIP_OK;
   if (a.n_head_kv <= 0 || a.n_head % a.n_head_kv != 0)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "head_count must be a multiple of head_count_kv");
   if (a.capacity <= 0) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "capacity must be positive");
+  if (!a.window) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "attention needs its key-window workspace");
+  if (attention_window_bytes(a) / 2 >= (1ull << 31))
+    return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "attention key window exceeds 2 GiB");
   switch (a.head_dim) {
     case 64: return launch_hd<64>(a, s);
     case 128: return launch_hd<128>(a, s);

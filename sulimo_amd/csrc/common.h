@@ -170,7 +170,11 @@ struct AttnArgs {
   const uint8_t *new_k, *new_v;
   long new_pos0;
   int start_pos, n, capacity, n_head, n_head_kv, head_dim;
+  // f16 copy of the visible key window (attention_window_bytes of device memory)
+  void *window;
 };
+// Device bytes of AttnArgs::window for this attention call.
+size_t attention_window_bytes(const AttnArgs &a);
 int32_t launch_attention(const AttnArgs &a, hipStream_t s);
 
 }  // namespace sulimo

@@ -219,6 +219,8 @@ int32_t sulimo_hip_enqueue_attention_prefill(sulimo_hip_ctx *ctx, const sulimo_h
   a.n_head = (int)head_count;
   a.n_head_kv = (int)head_count_kv;
   a.head_dim = (int)head_dim;
+  if ((rc = ensure_workspace(ctx, attention_window_bytes(a)))) return rc;
+  a.window = ctx->ws;
   wrote(out);
   return launch_attention(a, ctx->stream);
 }
@@ -423,7 +425,15 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   const bool want_argmax = outputs && outputs->argmax_all;
   const bool own_logits = want_argmax && !outputs->logits_all;
   const size_t chunk_rows = 256;
-  const size_t ws_need = off_l + (own_logits ? chunk_rows * V * 4 : 0);
+  // f16 copy of the attention key window (the same for every layer of the ubatch)
+  AttnArgs probe_at{};
+  probe_at.start_pos = (int)start_pos;
+  probe_at.n = (int)n;
+  probe_at.capacity = (int)cap;
+  probe_at.n_head_kv = (int)Hkv;
+  probe_at.head_dim = (int)hd;
+  const size_t off_w = off_l + ((own_logits ? chunk_rows * V * 4 : 0) + 255 & ~(size_t)255);
+  const size_t ws_need = off_w + attention_window_bytes(probe_at);
   if ((rc = ensure_workspace(ctx, ws_need))) return rc;
   char *ws = reinterpret_cast<char *>(ctx->ws);
   float *xres = reinterpret_cast<float *>(ws);
@@ -500,6 +510,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     at.n_head = (int)Hq;
     at.n_head_kv = (int)Hkv;
     at.head_dim = (int)hd;
+    at.window = ws + off_w;
     double keys = 0;  // sum over queries of visible keys
     for (size_t t = 0; t < n; t++) keys += (double)std::min(start_pos + t + 1, cap);
     const double kv_read = 2.0 * (double)std::min(start_pos + n, cap) * bpp;
