@@ -29,6 +29,7 @@
 //     Tiles that a wave cannot see are skipped; masks are applied only on the
 //     tiles that cross the causal diagonal or the window start.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -232,66 +233,102 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
   for (int i = 0; i < OT; i++) o[i] = floatx16{};
   float mrun = -INFINITY, lrun = 0.0f;
 
-  auto compute = [&](const char *sk, const char *sv, int tile) __attribute__((always_inline)) {
-    const int p0 = (int)wlo + tile * kKT;  // absolute position of the tile's first key
-    if (tile > te || !wave_live || p0 > Pw_max || p0 + kKT - 1 <= Pw_min - cap) return;  // nothing visible
-    const bool full = p0 + kKT - 1 <= Pw_min && p0 > Pw_max - cap;
-    // two halves of 32 keys, each a full online-softmax step
+  // --- one tile of 64 keys, as two 32-key online-softmax steps, software-pipelined so
+  // that the MFMAs of one step run under the VALU softmax of the other:
+  //   S0 | S1 + softmax0 | PV0 + softmax1 | PV1
+  auto s_step = [&](const char *sk, int kt, floatx16 &st) __attribute__((always_inline)) {
+    st = floatx16{};
+    const int row = 32 * kt + l32;
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-      __builtin_amdgcn_sched_barrier(0);  // bounds the live ranges the scheduler may stretch
-      floatx16 st = floatx16{};
-      const int row = 32 * kt + l32;
+    for (int s = 0; s < KS; s++) {
+      const int pos = (2 * s + lg) ^ (row % KCH);
+      const half8 kf = *reinterpret_cast<const half8 *>(sk + row * KROW + 16 * pos);
+      st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
+    }
+  };
+  auto pv_step = [&](const char *sv, int kt, const half8 (&pbk)[2]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int s = 0; s < KS; s++) {
-        const int pos = (2 * s + lg) ^ (row % KCH);
-        const half8 kf = *reinterpret_cast<const half8 *>(sk + row * KROW + 16 * pos);
-        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[s], st, 0, 0, 0);
-      }
-      if (!full) {  // wave-uniform; the per-key test is a select
-        const int pk = p0 + 32 * kt + 4 * lg;  // key of register 0 of this lane
+    for (int jh = 0; jh < 2; jh++) {
+      const int j = 2 * kt + jh;  // 16-key step of the tile
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int p = pk + 8 * (r >> 2) + (r & 3);
-          st[r] = (p > P || p <= P - cap) ? -INFINITY : st[r];
-        }
-      }
-      float mt = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float mnew = fmaxf(mrun, mt * c);
-      // a query that sees no key yet keeps m = -inf; msafe keeps exp2 finite so that
-      // every lane runs the same MFMA sequence
-      const float msafe = mnew == -INFINITY ? 0.0f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(mrun - msafe);
-      mrun = mnew;
-      half8 pb[2];
-      float lsum = 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], c, -msafe));
-        lsum += e;
-        pb[r >> 3][r & 7] = (_Float16)e;
-      }
-      lrun = lrun * alpha + lsum;
-      __builtin_amdgcn_sched_barrier(0);
-      if (__ballot(alpha != 1.0f)) {
-#pragma unroll
-        for (int i = 0; i < OT; i++) o[i] *= alpha;
-      }
-#pragma unroll
-      for (int jh = 0; jh < 2; jh++) {
-        const int j = 2 * kt + jh;  // 16-key step of the tile
-#pragma unroll
-        for (int i = 0; i < OT; i++) {
-          const int hr = 32 * i + l32;
-          const int pos = (2 * j + lg) ^ ((hr >> 1) & 7);
-          const half8 vf = *reinterpret_cast<const half8 *>(sv + hr * (kKT * 2) + 16 * pos);
-          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb[jh], o[i], 0, 0, 0);
-        }
+      for (int i = 0; i < OT; i++) {
+        const int hr = 32 * i + l32;
+        const int pos = (2 * j + lg) ^ ((hr >> 1) & 7);
+        const half8 vf = *reinterpret_cast<const half8 *>(sv + hr * (kKT * 2) + 16 * pos);
+        o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pbk[jh], o[i], 0, 0, 0);
       }
     }
+  };
+  // mask (diagonal / window-start tiles only), running max, exp2, sum, P^T as f16
+  auto softmax = [&](floatx16 &st, int p_reg0, bool masked, half8 (&pbk)[2]) __attribute__((always_inline)) -> float {
+    if (masked) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int p = p_reg0 + 8 * (r >> 2) + (r & 3);
+        st[r] = (p > P || p <= P - cap) ? -INFINITY : st[r];
+      }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mnew = fmaxf(mrun, mt * c);
+    // a query that sees no key yet keeps m = -inf; msafe keeps exp2 finite so that
+    // every lane runs the same MFMA sequence
+    const float msafe = mnew == -INFINITY ? 0.0f : mnew;
+    const float alpha = __builtin_amdgcn_exp2f(mrun - msafe);
+    mrun = mnew;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], c, -msafe));
+      lsum += e;
+      pbk[r >> 3][r & 7] = (_Float16)e;
+    }
+    lrun = lrun * alpha + lsum;
+    return alpha;
+  };
+  auto rescale = [&](float alpha) __attribute__((always_inline)) {
+    if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+      for (int i = 0; i < OT; i++) o[i] *= alpha;
+    }
+  };
+  // MFMA / VALU / LDS-read interleave of one pipelined phase (8 MFMAs)
+  auto interleave = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // 6 VALU
+    }
+  };
+  auto compute = [&](const char *sk, const char *sv, int tile, auto kMasked) __attribute__((always_inline)) {
+    constexpr bool M = decltype(kMasked)::value;
+    const int p0 = (int)wlo + tile * kKT;  // absolute position of the tile's first key
+    floatx16 st0, st1;
+    half8 pa[2], pbv[2];
+    s_step(sk, 0, st0);
+    __builtin_amdgcn_sched_barrier(0);
+    s_step(sk, 1, st1);
+    const float al0 = softmax(st0, p0 + 4 * lg, M, pa);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    rescale(al0);
+    __builtin_amdgcn_sched_barrier(0);
+    pv_step(sv, 0, pa);
+    const float al1 = softmax(st1, p0 + 32 + 4 * lg, M, pbv);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    rescale(al1);
+    __builtin_amdgcn_sched_barrier(0);
+    pv_step(sv, 1, pbv);
+  };
+  auto tile_work = [&](const char *sk, const char *sv, int tile) __attribute__((always_inline)) {
+    const int p0 = (int)wlo + tile * kKT;
+    if (tile > te || !wave_live || p0 > Pw_max || p0 + kKT - 1 <= Pw_min - cap) return;  // nothing visible
+    if (p0 + kKT - 1 <= Pw_min && p0 > Pw_max - cap) compute(sk, sv, tile, std::false_type{});
+    else compute(sk, sv, tile, std::true_type{});
   };
 
   // Per step: wait for this half's tile, barrier (it landed for all waves, and every
@@ -305,18 +342,18 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
       issue(k1, v1, tb + s + 1);
-      compute(k0, v0, tb + s);
+      tile_work(k0, v0, tb + s);
       wait_vmcnt0();
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
       issue(k0, v0, tb + s + 2);
-      compute(k1, v1, tb + s + 1);
+      tile_work(k1, v1, tb + s + 1);
     }
     if (s < nsteps) {
       wait_vmcnt0();
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      compute(k0, v0, tb + s);
+      tile_work(k0, v0, tb + s);
     }
   };
   if (half == 0) run(ka0, va0, ka1, va1);

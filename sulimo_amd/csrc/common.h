@@ -151,9 +151,12 @@ int32_t launch_embed_q4_0(const uint16_t *scales, const uint8_t *quants, const u
                           int n, int embd, uint16_t *x, hipStream_t s);
 // RoPE on q (in place, f16) and k (f32 rotation), then Q8_0 of k and v into
 // k_dst/v_dst rows of `dst_stride` bytes; row t goes to slot (slot0 + t) % wrap.
+// cos/sin table of a ubatch for the fused RoPE: float2 [n][rope_dim/2] at positions
+// start_pos .. start_pos+n-1.
+int32_t launch_rope_table(float *tab, int rope_dim, float freq_base, int start_pos, int n, hipStream_t s);
 int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v, int n_head,
-                              int n_head_kv, int head_dim, int rope_dim, float freq_base,
-                              int mode, int start_pos, int n, uint8_t *k_dst, uint8_t *v_dst,
+                              int n_head_kv, int head_dim, int rope_dim, const float *cs_tab,
+                              int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
                               int slot0, int wrap, hipStream_t s);
 // Copies n rows of `row_bytes` from src to ring slots (slot0 + t) % capacity.
 int32_t launch_ring_commit(const uint8_t *src, uint8_t *ring, size_t row_bytes, int slot0,

@@ -433,7 +433,9 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   probe_at.n_head_kv = (int)Hkv;
   probe_at.head_dim = (int)hd;
   const size_t off_w = off_l + ((own_logits ? chunk_rows * V * 4 : 0) + 255 & ~(size_t)255);
-  const size_t ws_need = off_w + attention_window_bytes(probe_at);
+  // RoPE cos/sin table of the ubatch (shared by all layers)
+  const size_t off_r = off_w + (attention_window_bytes(probe_at) + 255 & ~(size_t)255);
+  const size_t ws_need = off_r + n * (size_t)(cfg->rope_dim / 2) * 8;
   if ((rc = ensure_workspace(ctx, ws_need))) return rc;
   char *ws = reinterpret_cast<char *>(ctx->ws);
   float *xres = reinterpret_cast<float *>(ws);
@@ -454,6 +456,11 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     wrote(outputs->argmax_all);
   }
   if ((rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D, [&] { return launch_f16_to_f32(dp<const uint16_t>(scratch->x), xres, n * D, s); }))) return rc;
+  float *rope_tab = reinterpret_cast<float *>(ws + off_r);
+  if ((rc = timed(ctx, PROF_ROPE_KV, 0, 8.0 * n * (cfg->rope_dim / 2), [&] {
+         return launch_rope_table(rope_tab, cfg->rope_dim, cfg->rope_base, (int)start_pos, in, s);
+       })))
+    return rc;
   for (size_t l = 0; l < L; l++) {
     const sulimo_hip_layer_tensors &T = tensors->layers[l];
     uint8_t *ring_k = dp<uint8_t>(kv->k_buffers[l]);
@@ -490,7 +497,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     if ((rc = timed(ctx, PROF_ROPE_KV, 0, 2.0 * n * (qd + 2 * kvd) + 2.0 * n * qd + 2.0 * n * bpp, [&] {
            return launch_rope_qkv_store(dp<uint16_t>(scratch->q), dp<const uint16_t>(scratch->k),
                                         dp<const uint16_t>(scratch->v), (int)Hq, (int)Hkv, (int)hd,
-                                        cfg->rope_dim, cfg->rope_base, cfg->rope_mode, (int)start_pos, in,
+                                        cfg->rope_dim, rope_tab, cfg->rope_mode, in,
                                         staged ? stg_k : ring_k, staged ? stg_v : ring_v,
                                         staged ? 0 : (int)(start_pos % cap), staged ? in : (int)cap, s);
          })))

@@ -25,7 +25,50 @@ __device__ __forceinline__ float half_wave_max(float v) {
 __device__ __forceinline__ float load_f(const _Float16 *p, size_t i) { return (float)p[i]; }
 __device__ __forceinline__ float load_f(const float *p, size_t i) { return p[i]; }
 
-// One wave per row: out = f16(x * (1/sqrt(mean(x^2)+eps)) * w).
+// Four consecutive elements of x as f32 (16-byte f32 or 8-byte f16 load).
+__device__ __forceinline__ float4 load4(const float *p, size_t i) { return *reinterpret_cast<const float4 *>(p + i); }
+__device__ __forceinline__ float4 load4(const _Float16 *p, size_t i) {
+  typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+  const half4v h = *reinterpret_cast<const half4v *>(p + i);
+  return float4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
+// Row width d = 256 * V: one wave per row, the row held in registers between the sum of
+// squares and the scaling (one HBM read of x), 16-byte loads, 8-byte f16 stores.
+template <typename T, int V>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const T *__restrict__ x, const float *__restrict__ w,
+                                                          _Float16 *__restrict__ out,
+                                                          _Float16 *__restrict__ x16_out, float eps, int n) {
+  typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+  constexpr int D = 256 * V;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n) return;
+  const T *xr = x + (size_t)row * D;
+  float4 v[V];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    v[j] = load4(xr, 256 * j + 4 * lane);
+    ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+  }
+  ss = wave_sum(ss);
+  const float scale = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const int i = 256 * j + 4 * lane;
+    const float4 wv = *reinterpret_cast<const float4 *>(w + i);
+    const half4v o = {(_Float16)(v[j].x * scale * wv.x), (_Float16)(v[j].y * scale * wv.y),
+                      (_Float16)(v[j].z * scale * wv.z), (_Float16)(v[j].w * scale * wv.w)};
+    *reinterpret_cast<half4v *>(out + (size_t)row * D + i) = o;
+    if (x16_out) {
+      const half4v h = {(_Float16)v[j].x, (_Float16)v[j].y, (_Float16)v[j].z, (_Float16)v[j].w};
+      *reinterpret_cast<half4v *>(x16_out + (size_t)row * D + i) = h;
+    }
+  }
+}
+
+// Any width: one wave per row: out = f16(x * (1/sqrt(mean(x^2)+eps)) * w).
 // With x16_out, also writes f16(x) (final residual hand-back).
 template <typename T>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const T *__restrict__ x,
@@ -58,6 +101,18 @@ __device__ __forceinline__ void rope_cs(int pos, int i, int rope_dim, float base
   float freq = 1.0f / powf(base, (float)(2 * i) / (float)rope_dim);
   float theta = (float)pos * freq;
   sincosf(theta, &s, &c);
+}
+
+// cos/sin of every (position, pair) of a ubatch, [n][rope_dim/2]: the same values
+// rope_cs gives, computed once and shared by all heads and layers.
+__global__ void rope_table_kernel(float2 *tab, int rope_dim, float base, int start_pos, int n) {
+  const int half = rope_dim / 2;
+  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (long)n * half) return;
+  const int t = (int)(gid / half), i = (int)(gid % half);
+  float c, sn;
+  rope_cs(start_pos + t, i, rope_dim, base, c, sn);
+  tab[gid] = float2{c, sn};
 }
 
 // One thread per (token, head, pair): in-place f16 rotation.
@@ -152,7 +207,7 @@ __global__ void embed_q4_kernel(const uint16_t *scales, const uint8_t *quants,
 // the rest v heads (Q8_0 of the f16 values). head_dim <= 256, multiple of 32.
 __global__ __launch_bounds__(256) void rope_qkv_store_kernel(
     _Float16 *q, const _Float16 *k, const _Float16 *v, int n_head, int n_head_kv, int head_dim,
-    int rope_dim, float base, int mode, int start_pos, int n, uint8_t *k_dst, uint8_t *v_dst,
+    int rope_dim, const float2 *cs_tab, int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
     int slot0, int wrap) {
   __shared__ float sh[4][256];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -161,7 +216,6 @@ __global__ __launch_bounds__(256) void rope_qkv_store_kernel(
   if (job >= (long)n * slots) return;  // whole waves exit; no block barrier below
   const int t = (int)(job / slots), hs = (int)(job % slots);
   float *buf = sh[wave];
-  const int pos = start_pos + t;
   const int half = rope_dim / 2;
   const int kvd = n_head_kv * head_dim;
   const size_t row_bytes = (size_t)n_head_kv * (head_dim / 32) * 34;
@@ -174,8 +228,8 @@ __global__ __launch_bounds__(256) void rope_qkv_store_kernel(
     for (int i = lane; i < head_dim; i += 64) buf[i] = (float)hp[i];
     __builtin_amdgcn_wave_barrier();
     for (int i = lane; i < half; i += 64) {
-      float c, s;
-      rope_cs(pos, i, rope_dim, base, c, s);
+      const float2 cs = cs_tab[(size_t)t * half + i];
+      const float c = cs.x, s = cs.y;
       const int i0 = mode == 0 ? 2 * i : i;
       const int i1 = mode == 0 ? 2 * i + 1 : i + half;
       const float v0 = buf[i0], v1 = buf[i1];
@@ -247,22 +301,37 @@ inline unsigned blocks_for(size_t total, unsigned bs) { return (unsigned)((total
 
 }  // namespace
 
+namespace {
+// RMSNorm launch: the register-resident kernel for d = 256 * {1..16} (the hidden sizes
+// of the supported models), the generic one otherwise.
+template <typename T>
+int32_t launch_rmsnorm_t(const T *x, const float *w, _Float16 *out, _Float16 *x16_out, int d, float eps, int n,
+                         hipStream_t s) {
+  if (n <= 0) return SULIMO_HIP_OK;
+  const dim3 grid((n + 3) / 4), block(256);
+  switch (d % 256 == 0 ? d / 256 : 0) {
+#define SULIMO_RMS_CASE(V) \
+  case V: hipLaunchKernelGGL((rmsnorm_vec_kernel<T, V>), grid, block, 0, s, x, w, out, x16_out, eps, n); break;
+    SULIMO_RMS_CASE(1) SULIMO_RMS_CASE(2) SULIMO_RMS_CASE(3) SULIMO_RMS_CASE(4) SULIMO_RMS_CASE(5)
+    SULIMO_RMS_CASE(6) SULIMO_RMS_CASE(8) SULIMO_RMS_CASE(10) SULIMO_RMS_CASE(12) SULIMO_RMS_CASE(14)
+    SULIMO_RMS_CASE(16)
+#undef SULIMO_RMS_CASE
+    default: hipLaunchKernelGGL(rmsnorm_kernel<T>, grid, block, 0, s, x, w, out, x16_out, d, eps, n); break;
+  }
+  return check_launch("rmsnorm_kernel");
+}
+}  // namespace
+
 int32_t launch_rmsnorm_f16(const uint16_t *x, const float *w, uint16_t *out, int d, float eps,
                            int n, hipStream_t s) {
-  if (n <= 0) return SULIMO_HIP_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel<_Float16>, dim3((n + 3) / 4), dim3(256), 0, s,
-                     reinterpret_cast<const _Float16 *>(x), w, reinterpret_cast<_Float16 *>(out),
-                     (_Float16 *)nullptr, d, eps, n);
-  return check_launch("rmsnorm_kernel<f16>");
+  return launch_rmsnorm_t(reinterpret_cast<const _Float16 *>(x), w, reinterpret_cast<_Float16 *>(out),
+                          (_Float16 *)nullptr, d, eps, n, s);
 }
 
 int32_t launch_rmsnorm_f32(const float *x, const float *w, uint16_t *out, uint16_t *x16_out, int d,
                            float eps, int n, hipStream_t s) {
-  if (n <= 0) return SULIMO_HIP_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3((n + 3) / 4), dim3(256), 0, s, x, w,
-                     reinterpret_cast<_Float16 *>(out), reinterpret_cast<_Float16 *>(x16_out), d,
-                     eps, n);
-  return check_launch("rmsnorm_kernel<f32>");
+  return launch_rmsnorm_t(x, w, reinterpret_cast<_Float16 *>(out), reinterpret_cast<_Float16 *>(x16_out), d, eps,
+                          n, s);
 }
 
 int32_t launch_rope_f16(uint16_t *vec, int head_count, int head_dim, int rope_dim,
@@ -326,9 +395,17 @@ int32_t launch_embed_q4_0(const uint16_t *scales, const uint8_t *quants, const u
   return check_launch("embed_q4_kernel");
 }
 
+int32_t launch_rope_table(float *tab, int rope_dim, float freq_base, int start_pos, int n, hipStream_t s) {
+  const size_t total = (size_t)n * (rope_dim / 2);
+  if (total == 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(rope_table_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s,
+                     reinterpret_cast<float2 *>(tab), rope_dim, freq_base, start_pos, n);
+  return check_launch("rope_table_kernel");
+}
+
 int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v, int n_head,
-                              int n_head_kv, int head_dim, int rope_dim, float freq_base,
-                              int mode, int start_pos, int n, uint8_t *k_dst, uint8_t *v_dst,
+                              int n_head_kv, int head_dim, int rope_dim, const float *cs_tab,
+                              int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
                               int slot0, int wrap, hipStream_t s) {
   if (head_dim > 256 || head_dim % 32 != 0)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "head_dim must be a multiple of 32 and <= 256");
@@ -337,7 +414,7 @@ int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v,
   hipLaunchKernelGGL(rope_qkv_store_kernel, dim3(blocks_for(jobs, 4)), dim3(256), 0, s,
                      reinterpret_cast<_Float16 *>(q), reinterpret_cast<const _Float16 *>(k),
                      reinterpret_cast<const _Float16 *>(v), n_head, n_head_kv, head_dim, rope_dim,
-                     freq_base, mode, start_pos, n, k_dst, v_dst, slot0, wrap);
+                     reinterpret_cast<const float2 *>(cs_tab), mode, n, k_dst, v_dst, slot0, wrap);
   return check_launch("rope_qkv_store_kernel");
 }
 
