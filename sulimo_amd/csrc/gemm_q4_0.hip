@@ -100,8 +100,8 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int FM, int FN, int kNS, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
+template <int FM, int FN, int kNS, int EPI, int KSPLIT>
+__global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmArgs a) {
   constexpr int BM = 32 * FM;
   constexpr int BN = 128 * FN;                    // weight rows per tile (4 waves)
   constexpr bool kSwiglu = (EPI == EPI_SWIGLU);
@@ -115,24 +115,44 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
   constexpr int SLOT = X_BYTES + Q_BYTES + S_BYTES;
   static_assert(!kSwiglu || FN % 2 == 0, "SwiGLU pairs gate and up fragments in one wave");
   static_assert(kNS >= 2 && kNS <= 6, "ring depth");
+  static_assert(KSPLIT == 1 || KSPLIT == 2, "k split");
 
+  // Ring slots of the (first) k half, and of the second when the workgroup splits K.
   __shared__ __attribute__((aligned(16))) char smem0[SLOT];
   __shared__ __attribute__((aligned(16))) char smem1[SLOT];
   __shared__ __attribute__((aligned(16))) char smem2[kNS > 2 ? SLOT : 16];
   __shared__ __attribute__((aligned(16))) char smem3[kNS > 3 ? SLOT : 16];
   __shared__ __attribute__((aligned(16))) char smem4[kNS > 4 ? SLOT : 16];
   __shared__ __attribute__((aligned(16))) char smem5[kNS > 5 ? SLOT : 16];
-  auto slot_ptr = [&](auto J) -> char * {
+  constexpr int SLOT2 = KSPLIT > 1 ? SLOT : 16;
+  __shared__ __attribute__((aligned(16))) char smemb0[SLOT2];
+  __shared__ __attribute__((aligned(16))) char smemb1[SLOT2];
+  __shared__ __attribute__((aligned(16))) char smemb2[kNS > 2 ? SLOT2 : 16];
+  __shared__ __attribute__((aligned(16))) char smemb3[kNS > 3 ? SLOT2 : 16];
+  __shared__ __attribute__((aligned(16))) char smemb4[kNS > 4 ? SLOT2 : 16];
+  __shared__ __attribute__((aligned(16))) char smemb5[kNS > 5 ? SLOT2 : 16];
+  __shared__ __attribute__((aligned(16))) float comb[KSPLIT > 1 ? 256 * 16 : 4];  // one fragment of the second half
+  auto slot_ptr = [&](auto H, auto J) -> char * {
     constexpr int j = decltype(J)::value % kNS;
-    if constexpr (j == 0) return smem0;
-    else if constexpr (j == 1) return smem1;
-    else if constexpr (j == 2) return smem2;
-    else if constexpr (j == 3) return smem3;
-    else if constexpr (j == 4) return smem4;
-    else return smem5;
+    if constexpr (decltype(H)::value == 0) {
+      if constexpr (j == 0) return smem0;
+      else if constexpr (j == 1) return smem1;
+      else if constexpr (j == 2) return smem2;
+      else if constexpr (j == 3) return smem3;
+      else if constexpr (j == 4) return smem4;
+      else return smem5;
+    } else {
+      if constexpr (j == 0) return smemb0;
+      else if constexpr (j == 1) return smemb1;
+      else if constexpr (j == 2) return smemb2;
+      else if constexpr (j == 3) return smemb3;
+      else if constexpr (j == 4) return smemb4;
+      else return smemb5;
+    }
   };
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave = wave within its k half (4 per half); kh = the half of the K range it runs
+  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, kh = tid >> 8;
   const int l32 = lane & 31, lg = lane >> 5;
 
   // --- workgroup -> tile. Workgroups are dispatched round-robin over the XCDs, each with
@@ -206,9 +226,9 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
 
   // Always NDMA instructions, so vmcnt counts stay exact (stages past the end reload
   // stage 0). kCheck: the stage may be the half stage of an odd block count.
-  auto issue = [&](auto J, int st, auto kCheck) {
+  auto issue = [&](auto H, auto J, int st, auto kCheck) __attribute__((always_inline)) {
     const int sst = st < nst ? st : 0;
-    char *slot = slot_ptr(J);
+    char *slot = slot_ptr(H, J);
     bool half = false;
     if constexpr (decltype(kCheck)::value) half = (2 * sst + 1 == nb);
 #pragma unroll
@@ -243,8 +263,10 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
         acc[i][f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao[i], bo[f], acc[i][f], 0, 0, 0);
   };
 
-  // One stage in slot J. kCheck: the stage or the one it prefetches may be the half stage.
-  auto stage = [&](auto J, int st, auto kCheck) {
+  // One stage in slot J of half H. kCheck: the stage or the one it prefetches may be
+  // the half stage. An inactive stage (past the half's range) only keeps the ring and the
+  // barrier count in step.
+  auto stage = [&](auto H, auto J, int st, auto kCheck, bool active) __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
     // stage st was issued NS-1 stages ago, (NS-2)*NDMA DMA instructions after it
     wait_vmcnt<(kNS - 2) * NDMA>();
@@ -252,8 +274,9 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
     // reads were consumed by its MFMAs; a fenced barrier would drain every prefetch
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue(ic<decltype(J)::value + kNS - 1>{}, st + kNS - 1, kCheck);  // refills the slot of stage st-1
-    const char *slot = slot_ptr(J);
+    issue(H, ic<decltype(J)::value + kNS - 1>{}, st + kNS - 1, kCheck);  // refills the slot of stage st-1
+    if (!active) return;
+    const char *slot = slot_ptr(H, J);
     const _Float16 *xb = reinterpret_cast<const _Float16 *>(slot);
     // raw weights of this wave's fragments: 8 bytes per block, and the stage's 2 scales
     uint2 q[FN][2];
@@ -300,22 +323,59 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
     mfmas(a1, b1);
   };
 
-  // Main loop: straight-line bodies of NS stages (no branches between stages keeps the
-  // wait analysis per slot) over the stages whose prefetch target is a full stage.
+  // Each k half runs nst_h stages [sb, sb + nst_h) of the K range (the last half fewer
+  // real ones). Main loop: straight-line bodies of NS stages (no branches between
+  // stages keeps the wait analysis per slot) over the stages that are active, full, and
+  // prefetch no half stage; the rest go through the checked tail. Every half runs the
+  // same number of stages, hence of barriers.
   using yes = std::true_type;
   using no = std::false_type;
-  static_for<kNS - 1>([&](auto J) { issue(J, decltype(J)::value, yes{}); });
-  const int nfull = nb >> 1;
-  const int nsafe = (nb & 1) ? nfull - (kNS - 1) : nst;  // stages st < nsafe prefetch full stages
-  int st0 = 0;
-  for (; st0 + kNS <= nsafe; st0 += kNS)
-    static_for<kNS>([&](auto J) { stage(J, st0 + decltype(J)::value, no{}); });
-  // Tail: fewer than 2*NS stages, each checked.
-  static_for<2 * kNS - 1>([&](auto J) {
-    if (st0 + decltype(J)::value < nst) stage(J, st0 + decltype(J)::value, yes{});
-  });
+  const int nst_h = (nst + KSPLIT - 1) / KSPLIT;
+  auto run = [&](auto H) __attribute__((always_inline)) {
+    const int sb = decltype(H)::value * nst_h;
+    const int se = min(nst, sb + nst_h);
+    static_for<kNS - 1>([&](auto J) { issue(H, J, sb + decltype(J)::value, yes{}); });
+    int lim = se - sb;
+    if (nb & 1) lim = min(lim, nst - kNS - sb);  // stage nst-NS prefetches the half stage
+    lim = max(lim, 0);
+    int s0 = 0;
+    for (; s0 + kNS <= lim; s0 += kNS)
+      static_for<kNS>([&](auto J) { stage(H, J, sb + s0 + decltype(J)::value, no{}, true); });
+    static_for<2 * kNS>([&](auto J) {
+      const int st = sb + s0 + decltype(J)::value;
+      if (s0 + decltype(J)::value < nst_h) stage(H, J, st, yes{}, st < se);
+    });
+  };
+  if constexpr (KSPLIT == 1) {
+    run(ic<0>{});
+  } else {
+    if (kh == 0) run(ic<0>{});
+    else run(ic<1>{});
+  }
   // no DMA may still be writing this workgroup's LDS when it exits
   wait_vmcnt<0>();
+  if constexpr (KSPLIT > 1) {
+    // the second half hands its accumulators to the first, one fragment at a time
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int f = 0; f < FN; f++) {
+        float *cb = comb + (wave * 64 + lane) * 16;
+        if (kh) {
+#pragma unroll
+          for (int r = 0; r < 16; r += 4)
+            *reinterpret_cast<float4 *>(cb + r) = float4{acc[i][f][r], acc[i][f][r + 1], acc[i][f][r + 2], acc[i][f][r + 3]};
+        }
+        __syncthreads();
+        if (!kh) {
+#pragma unroll
+          for (int r = 0; r < 16; r++) acc[i][f][r] += cb[r];
+        }
+        __syncthreads();
+      }
+    if (kh) return;
+  }
 
   // --- epilogue: acc register r of fragment (i, f) is C[8*(r/4) + 4*lg + r%4][l32] ---
 #pragma unroll
@@ -378,7 +438,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4_kernel(GemmArgs a) {
   }
 }
 
-template <int FM, int FN, int NS = 3>
+template <int FM, int FN, int NS = 3, int KSPLIT = 1>
 int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   constexpr int BM = 32 * FM;
   constexpr int BN = 128 * FN;
@@ -388,12 +448,12 @@ int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   for (int i = 0; i < a.nseg; i++) a.tiles_n += (a.seg[i].n + out_bn - 1) / out_bn;
   a.tiles_m = (a.m + BM - 1) / BM;
   a.group_m = 4;
-  const dim3 grid(a.tiles_m * a.tiles_n), block(256);
+  const dim3 grid(a.tiles_m * a.tiles_n), block(256 * KSPLIT);
   switch (a.epi) {
-    case EPI_F16: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F16>), grid, block, 0, s, a); break;
-    case EPI_F32: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F32>), grid, block, 0, s, a); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_RESID>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_SWIGLU>), grid, block, 0, s, a); break;
+    case EPI_F16: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F16, KSPLIT>), grid, block, 0, s, a); break;
+    case EPI_F32: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F32, KSPLIT>), grid, block, 0, s, a); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_RESID, KSPLIT>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_SWIGLU, KSPLIT>), grid, block, 0, s, a); break;
     default: return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "unknown GEMM epilogue");
   }
   const hipError_t e = hipGetLastError();
@@ -432,16 +492,22 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
   if (a.epi == EPI_SWIGLU && a.nseg != 1)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "SwiGLU GEMM takes one segment");
   // Tile choice: each weight is dequantized once per workgroup and reused for BM rows,
-  // and two workgroups share a CU. 128 x 256 tiles move the fewest bytes per MAC but
-  // only pay off when they fill the GPU at least twice over; otherwise 64 x 256.
-  if (a.m <= 32) return launch_cfg<1, 2>(a, s);   // 32 x 256
-  if (a.m <= 64) return launch_cfg<2, 2>(a, s);   // 64 x 256
-  int tiles128 = 0;
-  const int out128 = a.epi == EPI_SWIGLU ? 128 : 256;
-  for (int i = 0; i < a.nseg; i++) tiles128 += (a.seg[i].n + out128 - 1) / out128;
-  tiles128 *= (a.m + 127) / 128;
-  if (tiles128 >= 4 * cu_count()) return launch_cfg<4, 2>(a, s);  // 128 x 256
-  return launch_cfg<2, 2>(a, s);                            // 64 x 256
+  // and two workgroups (or one of 8 waves) share a CU. 128 x 256 tiles move the fewest
+  // bytes per MAC but only pay off when they fill the GPU at least twice over. Grids
+  // smaller than two workgroups per CU split K inside the workgroup (8 waves).
+  int ntn = 0;
+  const int out_bn = a.epi == EPI_SWIGLU ? 128 : 256;
+  for (int i = 0; i < a.nseg; i++) ntn += (a.seg[i].n + out_bn - 1) / out_bn;
+  const int cus = cu_count();
+  const bool split = a.k >= 256 * 2;  // at least two 64-wide stages per half
+  if (a.m <= 32) {
+    if (split && ntn < 2 * cus) return launch_cfg<1, 2, 3, 2>(a, s);  // 32 x 256, K in halves
+    return launch_cfg<1, 2>(a, s);                                     // 32 x 256
+  }
+  const int tiles64 = ntn * ((a.m + 63) / 64);
+  if (a.m > 64 && ntn * ((a.m + 127) / 128) >= 4 * cus) return launch_cfg<4, 2>(a, s);  // 128 x 256
+  if (split && tiles64 < 2 * cus) return launch_cfg<2, 2, 3, 2>(a, s);                 // 64 x 256, K in halves
+  return launch_cfg<2, 2>(a, s);                                                       // 64 x 256
 }
 
 }  // namespace sulimo
