@@ -25,10 +25,18 @@
 //                     max and sum are per-lane scalars (plus one swap with l^32);
 //       P = exp2(S c - m), c = log2(e)/sqrt(head_dim) folded into one fma;
 //       O^T += V^T P^T  V^T (LDS) as A, P^T straight from the S^T registers as B.
-//     The accumulator is rescaled only on tiles where some running max moved.
+//     The running max m only moves when a tile's max exceeds it by more than 2^8, so
+//     the accumulator is rescaled on few tiles (P <= 256, exact to f16 precision).
 //     Tiles that a wave cannot see are skipped; masks are applied only on the
 //     tiles that cross the causal diagonal or the window start.
+//     Causal work grows with the position, so a query block's key steps may be cut
+//     into pieces of at most C steps (C from a cost model of the workgroups, which
+//     also favours splitting few long blocks over many CUs): every workgroup runs
+//     one piece, heaviest blocks first. A block in one piece writes
+//     its f16 output; the pieces of a split block write (O, m, l) partials, and
+//  3. attn_merge_kernel combines them (the same rescale-and-add as the halves).
 #include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "common.h"
@@ -38,11 +46,16 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 constexpr int kKT = 64;  // keys per tile
+constexpr float kLazy = 8.0f;  // log2 growth of the running max before O is rescaled
+// V^T rows are wpad + kVPad positions apart: a 4 KB power-of-two row stride would send
+// all 128 rows of a tile to the same few L2 channels.
+constexpr int kVPad = 64;
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
 // Stored slot s of a 16-key group holds key kperm(s): slots 0-7 = keys {0-3, 8-11}
@@ -63,6 +76,16 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 __device__ __forceinline__ void wait_vmcnt0() { wait_vmcnt<0>(); }
+
+// Key steps of query block qblk (64-key tiles, two per step: one per half).
+__host__ __device__ inline int attn_block_steps(int qblk, int PB, int n, int start_pos, int cap, int wlo) {
+  const int tg0 = qblk * PB * 32;
+  const int tg_last = (tg0 + PB * 32 < n ? tg0 + PB * 32 : n) - 1;
+  const int jlo0 = start_pos + tg0 - cap + 1 - wlo;
+  const int jlo = jlo0 > 0 ? jlo0 : 0, jhi = start_pos + tg_last - wlo;
+  return (jhi / kKT - jlo / kKT + 2) / 2;
+}
+__host__ __device__ inline int attn_pieces(int steps, int C) { return (steps + C - 1) / C; }
 
 struct Window {
   long lo;    // absolute position of window index 0
@@ -130,16 +153,22 @@ __global__ __launch_bounds__(256) void kv_window_kernel(AttnArgs a, long wlo, in
     half8 v;
 #pragma unroll
     for (int e = 0; e < 8; e++) v[e] = vt[16 * (c >> 1) + kperm(8 * (c & 1) + e)][h];
-    *reinterpret_cast<half8 *>(vwin + ((size_t)kvh * HD + h) * wpad + j0 + 8 * c) = v;
+    *reinterpret_cast<half8 *>(vwin + ((size_t)kvh * HD + h) * (wpad + kVPad) + j0 + 8 * c) = v;
   }
 }
 
 // ---------------------------------------------------------------------------
 // 2. flash attention over the f16 window
 // ---------------------------------------------------------------------------
+// Split-key partial of one piece: per field, 256 floats (query wave x lane):
+// fields 0 .. 16*OT-1 = the O^T accumulator registers, then m, then the lane's l.
+template <int HD>
+constexpr int part_fields() { return 16 * (HD / 32) + 2; }
+
 template <int HD>
 __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo, int wpad, int HG, int PB,
-                                                            int n_qblk, int n_hgrp) {
+                                                            int n_qblk, int n_hgrp, int C, float *part,
+                                                            int pmax) {
   constexpr int KS = HD / 16;          // S^T k-steps over head_dim
   constexpr int OT = HD / 32;          // O^T tiles over head_dim
   constexpr int KCH = HD / 8;          // 16-byte chunks per K row
@@ -159,12 +188,20 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
   const int half = wave >> 2, qw = wave & 3;
   const int l32 = lane & 31, lg = lane >> 5;
 
-  // Heaviest position blocks first (causal work grows with the position).
-  int bid = blockIdx.x;
-  const int hgrp = bid % n_hgrp;
-  bid /= n_hgrp;
-  const int kvh = bid % a.n_head_kv;
-  const int qblk = n_qblk - 1 - bid / a.n_head_kv;
+  // workgroup -> (head group, query block, piece): heaviest blocks first, the pieces of
+  // a block consecutive, the head groups innermost
+  const int n_groups = a.n_head_kv * n_hgrp;
+  const int grp = blockIdx.x % n_groups;
+  const int hgrp = grp % n_hgrp, kvh = grp / n_hgrp;
+  int wi = blockIdx.x / n_groups;
+  int qblk = n_qblk - 1, npiece;
+  for (;;) {
+    npiece = attn_pieces(attn_block_steps(qblk, PB, a.n, a.start_pos, a.capacity, (int)wlo), C);
+    if (wi < npiece || qblk == 0) break;
+    wi -= npiece;
+    qblk--;
+  }
+  const int piece = wi;
   const int G = a.n_head / a.n_head_kv;
   const int hj = qw % HG, pb = qw / HG;
   const int h = kvh * G + hgrp * HG + hj;
@@ -196,16 +233,20 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
   // window indices j = p - wlo of the keys any query of the workgroup sees
   const int jlo = max(0, Pg_min - cap + 1 - (int)wlo), jhi = Pg_max - (int)wlo;  // inclusive
   const int tile0 = jlo / kKT, tile1 = jhi / kKT;                                 // inclusive
-  // the first half takes the first ceil(n/2) tiles, the second half the rest
+  // the first half takes the first ceil(n/2) tiles, the second half the rest; this
+  // piece runs steps [sa, sb) of both
   const int nsteps = (tile1 - tile0 + 2) / 2;
-  const int tb = half ? tile0 + nsteps : tile0;
-  const int te = half ? tile1 : tile0 + nsteps - 1;  // te < tb: nothing for this half
+  const int sa = piece * nsteps / npiece, sb = (piece + 1) * nsteps / npiece;
+  const int tb = (half ? tile0 + nsteps : tile0) + sa;
+  const int te = min(half ? tile1 : tile0 + nsteps - 1, tb + (sb - sa) - 1);  // te < tb: nothing for this half
+  const int psteps = sb - sa;
 
   // DMA sources (bytes): K rows and V^T rows of this kv head; the tile start goes in soffset.
   const _Float16 *kwin = reinterpret_cast<const _Float16 *>(a.window);
   const _Float16 *vwin = kwin + (size_t)a.n_head_kv * wpad * HD;
   const rsrc_t rk = make_rsrc(kwin + (size_t)kvh * wpad * HD, (uint32_t)wpad * HD * 2);
-  const rsrc_t rv = make_rsrc(vwin + (size_t)kvh * HD * wpad, (uint32_t)HD * wpad * 2);
+  const int vst = wpad + kVPad;  // V^T row stride (positions)
+  const rsrc_t rv = make_rsrc(vwin + (size_t)kvh * HD * vst, (uint32_t)HD * vst * 2);
   uint32_t koff[NKI], voff[NVI];
 #pragma unroll
   for (int i = 0; i < NKI; i++) {
@@ -217,7 +258,7 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
   for (int i = 0; i < NVI; i++) {
     const int hr = 8 * (NVI * qw + i) + lane / 8;
     const int ch = (lane % 8) ^ ((hr >> 1) & 7);
-    voff[i] = (uint32_t)(hr * wpad + 8 * ch) * 2u;
+    voff[i] = (uint32_t)(hr * vst + 8 * ch) * 2u;
   }
   // always issued (an idle half reloads a valid tile), so every wave waits the same way
   auto issue = [&](char *sk, char *sv, int tile) __attribute__((always_inline)) {
@@ -272,19 +313,26 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
 #pragma unroll
     for (int r = 0; r < 16; r++) mt = fmaxf(mt, st[r]);
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mnew = fmaxf(mrun, mt * c);
-    // a query that sees no key yet keeps m = -inf; msafe keeps exp2 finite so that
-    // every lane runs the same MFMA sequence
-    const float msafe = mnew == -INFINITY ? 0.0f : mnew;
-    const float alpha = __builtin_amdgcn_exp2f(mrun - msafe);
-    mrun = mnew;
+    // The running max only moves when the tile's max exceeds it by more than 2^8 (log2
+    // units): P = exp2(s c - m) then stays <= 256, exact to f16 precision, and O and l
+    // are rescaled on few tiles. Softmax is shift-invariant, so the result is the same.
+    // A query that sees no key yet keeps m = -inf (and O = l = 0).
+    const float mcand = mt * c;
+    const bool grow = mcand > mrun + kLazy;
+    const float alpha = (grow && mrun != -INFINITY) ? __builtin_amdgcn_exp2f(mrun - mcand) : 1.0f;
+    if (grow) mrun = mcand;
+    // msafe keeps exp2 finite so that every lane runs the same MFMA sequence
+    const float msafe = mrun == -INFINITY ? 0.0f : mrun;
+#pragma unroll
+    for (int r = 0; r < 16; r++) pbk[r >> 3][r & 7] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(st[r], c, -msafe));
+    // l sums the f16 P the MFMA consumes, two per dot2 with f32 accumulation
+    const half2v one2 = {(_Float16)1.0f, (_Float16)1.0f};
     float lsum = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], c, -msafe));
-      lsum += e;
-      pbk[r >> 3][r & 7] = (_Float16)e;
-    }
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        lsum = __builtin_amdgcn_fdot2(half2v{pbk[j][e], pbk[j][e + 1]}, one2, lsum, false);
     lrun = lrun * alpha + lsum;
     return alpha;
   };
@@ -337,7 +385,7 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
   auto run = [&](char *k0, char *v0, char *k1, char *v1) __attribute__((always_inline)) {
     issue(k0, v0, tb);
     int s = 0;
-    for (; s + 1 < nsteps; s += 2) {
+    for (; s + 1 < psteps; s += 2) {
       wait_vmcnt0();
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
@@ -349,7 +397,7 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
       issue(k0, v0, tb + s + 2);
       tile_work(k1, v1, tb + s + 1);
     }
-    if (s < nsteps) {
+    if (s < psteps) {
       wait_vmcnt0();
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
@@ -384,6 +432,7 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
         a0 = __builtin_amdgcn_exp2f(mrun - ms);
         a1 = __builtin_amdgcn_exp2f(m1 - ms);
         lrun = lrun * a0 + l1 * a1;
+        mrun = mm;  // O and l are now relative to the joint max (a split block's partial keeps it)
       }
 #pragma unroll
       for (int r = 0; r < 16; r++) o[i][r] = o[i][r] * a0 + comb[ci * 16 + r] * a1;
@@ -391,6 +440,18 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
     __syncthreads();
   }
   if (half) return;
+
+  if (npiece > 1) {  // a piece of a split block: its partial (O^T, m, l) for the merge
+    constexpr int NF = part_fields<HD>();
+    float *rec = part + (((size_t)grp * n_qblk + qblk) * pmax + piece) * (size_t)(NF * 256) + ci;
+#pragma unroll
+    for (int i = 0; i < OT; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) rec[(16 * i + r) * 256] = o[i][r];
+    rec[(16 * OT) * 256] = mrun;
+    rec[(16 * OT + 1) * 256] = lrun;
+    return;
+  }
 
   // --- normalize and store: lane holds O[t][32i + 8(r/4) + 4lg + r%4] ---
   float l = lrun + __shfl_xor(lrun, 32, 64);
@@ -407,6 +468,135 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
     }
 }
 
+// ---------------------------------------------------------------------------
+// 3. merge the pieces of split query blocks
+// ---------------------------------------------------------------------------
+// One workgroup = 4 waves per (head group, query block); wave qw and lane hold the
+// same queries and O^T registers as in flash_attn_kernel.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, long wlo, int HG, int PB, int n_qblk,
+                                                         int n_hgrp, int C, const float *part, int pmax) {
+  constexpr int OT = HD / 32;
+  constexpr int NF = part_fields<HD>();
+  constexpr int PMAX = 16;  // pieces combined per pass
+  const int qblk = blockIdx.x, grp = blockIdx.y, i = blockIdx.z;  // i: the O^T tile (32 head-dim rows)
+  const int npiece = attn_pieces(attn_block_steps(qblk, PB, a.n, a.start_pos, a.capacity, (int)wlo), C);
+  if (npiece < 2) return;  // written by flash_attn_kernel
+  const int lane = threadIdx.x & 63, qw = threadIdx.x >> 6, ci = threadIdx.x;
+  const int hgrp = grp % n_hgrp, kvh = grp / n_hgrp;
+  const int G = a.n_head / a.n_head_kv;
+  const int hj = qw % HG, pb = qw / HG;
+  const int h = kvh * G + hgrp * HG + hj;
+  const int t = (qblk * PB + pb) * 32 + (lane & 31);
+  const int lg = lane >> 5;
+  const float *rec0 = part + ((size_t)grp * n_qblk + qblk) * pmax * (size_t)(NF * 256) + ci;
+  // every load of a piece is issued before any is used
+  float m = -INFINITY, l = 0.0f, o[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) o[r] = 0.0f;
+  for (int p0 = 0; p0 < npiece; p0 += PMAX) {
+    const int np = min(PMAX, npiece - p0);
+    float mp[PMAX];
+#pragma unroll
+    for (int p = 0; p < PMAX; p++) mp[p] = p < np ? rec0[(size_t)(p0 + p) * NF * 256 + (16 * OT) * 256] : -INFINITY;
+    float mm = m;
+#pragma unroll
+    for (int p = 0; p < PMAX; p++) mm = fmaxf(mm, mp[p]);
+    const float ms = mm == -INFINITY ? 0.0f : mm;
+    const float a0 = __builtin_amdgcn_exp2f(m - ms);
+    l *= a0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[r] *= a0;
+    m = mm;
+    for (int p = 0; p < np; p++) {
+      const float *rec = rec0 + (size_t)(p0 + p) * NF * 256;
+      float v[17];
+#pragma unroll
+      for (int r = 0; r < 16; r++) v[r] = rec[(16 * i + r) * 256];
+      v[16] = rec[(16 * OT + 1) * 256];
+      const float sc = __builtin_amdgcn_exp2f(mp[p] - ms);
+      l += v[16] * sc;
+#pragma unroll
+      for (int r = 0; r < 16; r++) o[r] += v[r] * sc;
+    }
+  }
+  l += __shfl_xor(l, 32, 64);
+  if (t >= a.n) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  _Float16 *dst = reinterpret_cast<_Float16 *>(a.out) + (size_t)t * a.n_head * HD + (size_t)h * HD;
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const half4 v = {(_Float16)(o[4 * g] * inv), (_Float16)(o[4 * g + 1] * inv), (_Float16)(o[4 * g + 2] * inv),
+                     (_Float16)(o[4 * g + 3] * inv)};
+    *reinterpret_cast<half4 *>(dst + 32 * i + 8 * g + 4 * lg) = v;
+  }
+}
+
+// Work split of one attention call.
+struct AttnPlan {
+  int HG, PB, n_qblk, n_hgrp, C, pmax, pieces;  // pieces = workgroups per head group
+};
+
+AttnPlan plan_attention(const AttnArgs &a, const Window &w) {
+  AttnPlan p;
+  // 4 query waves = HG heads of one KV group x PB blocks of 32 positions, twice (the
+  // two halves of the key range)
+  const int G = a.n_head / a.n_head_kv;
+  p.HG = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
+  p.PB = 4 / p.HG;
+  p.n_qblk = (a.n + 32 * p.PB - 1) / (32 * p.PB);
+  p.n_hgrp = G / p.HG;
+  const int n_groups = a.n_head_kv * p.n_hgrp;
+  int maxs = 1;
+  for (int b = 0; b < p.n_qblk; b++)
+    maxs = std::max(maxs, attn_block_steps(b, p.PB, a.n, a.start_pos, a.capacity, (int)w.lo));
+  // Piece size from the workgroup costs measured on MI355X at head_dim 128: about 8 us
+  // fixed (Q load, first K/V tiles, merge of the halves) plus 2 us per step, one
+  // workgroup per compute unit; a split adds the merge kernel (about 3 us plus its
+  // partial traffic). Half the step cost at head_dim 64.
+  const double cus = device_cu_count();
+  const double f = 8.0, g = a.head_dim > 64 ? 2.0 : 1.0;
+  const double rec_bytes = (16.0 * (a.head_dim / 32) + 2) * 256 * 4;
+  auto cost = [&](int C, int *pieces, int *pmax) {
+    int np = 0, pm = 1, split_pieces = 0;
+    for (int b = 0; b < p.n_qblk; b++) {
+      const int k = attn_pieces(attn_block_steps(b, p.PB, a.n, a.start_pos, a.capacity, (int)w.lo), C);
+      np += k;
+      pm = std::max(pm, k);
+      if (k > 1) split_pieces += k;
+    }
+    *pieces = np;
+    *pmax = pm;
+    const double rounds = std::ceil((double)np * n_groups / cus);
+    double t = rounds * (f + g * std::min(C, maxs));
+    if (pm > 1) t += 3.0 + (double)split_pieces * n_groups * rec_bytes * 2 / 4e12 * 1e6;
+    return t;
+  };
+  p.C = maxs;
+  double best = cost(maxs, &p.pieces, &p.pmax);
+  for (int C = 2; C < maxs; C++) {
+    int np, pm;
+    const double t = cost(C, &np, &pm);
+    if (t < best * 0.97) {  // split only for a clear gain
+      best = t;
+      p.C = C;
+      p.pieces = np;
+      p.pmax = pm;
+    }
+  }
+  return p;
+}
+
+size_t window_bytes(const AttnArgs &a, const Window &w) {
+  return ((size_t)a.n_head_kv * a.head_dim * (2 * (size_t)w.pad + kVPad) * 2 + 255) & ~(size_t)255;
+}
+
+size_t partial_bytes(const AttnArgs &a, const AttnPlan &p) {
+  if (p.pmax < 2) return 0;
+  const size_t nf = 16 * (size_t)(a.head_dim / 32) + 2;
+  return (size_t)a.n_head_kv * p.n_hgrp * p.n_qblk * p.pmax * nf * 256 * 4;
+}
+
 template <int HD>
 int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
   const Window w = window_of(a);
@@ -414,24 +604,26 @@ int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
                      w.pad);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "kv_window_kernel launch");
-  // 4 query waves = HG heads of one KV group x PB blocks of 32 positions, twice (the
-  // two halves of the key range)
-  const int G = a.n_head / a.n_head_kv;
-  const int HG = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
-  const int PB = 4 / HG;
-  const int n_qblk = (a.n + 32 * PB - 1) / (32 * PB);
-  const int n_hgrp = G / HG;
-  hipLaunchKernelGGL((flash_attn_kernel<HD>), dim3(n_qblk * a.n_head_kv * n_hgrp), dim3(512), 0, s, a, w.lo, w.pad,
-                     HG, PB, n_qblk, n_hgrp);
+  const AttnPlan p = plan_attention(a, w);
+  float *part = reinterpret_cast<float *>(reinterpret_cast<char *>(a.window) + window_bytes(a, w));
+  const int n_groups = a.n_head_kv * p.n_hgrp;
+  hipLaunchKernelGGL((flash_attn_kernel<HD>), dim3(p.pieces * n_groups), dim3(512), 0, s, a, w.lo, w.pad, p.HG, p.PB,
+                     p.n_qblk, p.n_hgrp, p.C, part, p.pmax);
   e = hipGetLastError();
-  return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "flash_attn_kernel launch");
+  if (e != hipSuccess) return hip_fail(e, "flash_attn_kernel launch");
+  if (p.pmax < 2) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(p.n_qblk, n_groups, HD / 32), dim3(256), 0, s, a, w.lo, p.HG, p.PB,
+                     p.n_qblk, p.n_hgrp, p.C, part, p.pmax);
+  e = hipGetLastError();
+  return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "attn_merge_kernel launch");
 }
 
 }  // namespace
 
-size_t attention_window_bytes(const AttnArgs &a) {
+size_t attention_workspace_bytes(const AttnArgs &a) {
+  if (a.n <= 0 || a.n_head_kv <= 0 || a.n_head % a.n_head_kv != 0 || a.capacity <= 0) return 0;
   const Window w = window_of(a);
-  return 2 * (size_t)a.n_head_kv * w.pad * a.head_dim * 2;
+  return window_bytes(a, w) + partial_bytes(a, plan_attention(a, w));
 }
 
 int32_t launch_attention(const AttnArgs &a, hipStream_t s) {
@@ -440,7 +632,7 @@ int32_t launch_attention(const AttnArgs &a, hipStream_t s) {
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "head_count must be a multiple of head_count_kv");
   if (a.capacity <= 0) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "capacity must be positive");
   if (!a.window) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "attention needs its key-window workspace");
-  if (attention_window_bytes(a) / 2 >= (1ull << 31))
+  if (window_bytes(a, window_of(a)) / 2 >= (1ull << 31))
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "attention key window exceeds 2 GiB");
   switch (a.head_dim) {
     case 64: return launch_hd<64>(a, s);

@@ -91,6 +91,7 @@ enum GemmEpilogue : int {
   EPI_F32 = 1,     // out f32 [rows][ldo]
   EPI_RESID = 2,   // out f32 residual [rows][ldo] += f16(acc)
   EPI_SWIGLU = 3,  // out f16 [rows][ldo] = silu(acc_w0) * acc_w1 (w0 = gate, w1 = up)
+  EPI_PART = 4,    // f32 partial sums of one K split: part[split][rows][ldp], reduced by a later kernel
 };
 
 // One weight matrix of a (possibly segmented) GEMM: `n` output rows, its
@@ -111,12 +112,21 @@ struct GemmArgs {
   int epi;
   GemmSegment seg[3];
   int nseg;
+  // K split across workgroups (EPI_PART only): `splits` workgroups per tile, split s
+  // covering k stages [s * split_stages, (s + 1) * split_stages) of 64, each writing its
+  // partial sums to part + s * m * ldp, column = (columns of the segments before) + col.
+  int splits, split_stages;
+  float *part;
+  int ldp;
   // Tile grid, filled by the launcher: tiles_m x tiles_n tiles, visited in groups of
   // group_m tile rows.
   int tiles_m, tiles_n, group_m;
 };
 
 int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s);
+
+// Compute units of the current device (cached per device).
+int device_cu_count();
 
 // Bytes of one panel record: 32 weight rows x one 64-wide k stage (1 KB quants + 128 B scales).
 constexpr int kQ4PanelRecord = 1152;
@@ -173,11 +183,14 @@ struct AttnArgs {
   const uint8_t *new_k, *new_v;
   long new_pos0;
   int start_pos, n, capacity, n_head, n_head_kv, head_dim;
-  // f16 copy of the visible key window (attention_window_bytes of device memory)
+  // Attention workspace (attention_workspace_bytes of device memory): the f16 copy of
+  // the visible key window, then the partial results of query blocks whose keys are
+  // split over several workgroups.
   void *window;
 };
-// Device bytes of AttnArgs::window for this attention call.
-size_t attention_window_bytes(const AttnArgs &a);
+// Device bytes of AttnArgs::window for this attention call (depends on the shapes and
+// on the device's compute-unit count).
+size_t attention_workspace_bytes(const AttnArgs &a);
 int32_t launch_attention(const AttnArgs &a, hipStream_t s);
 
 }  // namespace sulimo

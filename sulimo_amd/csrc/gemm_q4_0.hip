@@ -32,6 +32,7 @@
 //    then refill the slot every wave finished reading in the previous stage.
 //  * An odd block count ends in a half stage: its second block has scale 0 in the
 //    panels and its X chunks past K are zero-filled.
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -155,23 +156,28 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
   const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, kh = tid >> 8;
   const int l32 = lane & 31, lg = lane >> 5;
 
-  // --- workgroup -> tile. Workgroups are dispatched round-robin over the XCDs, each with
-  // its own L2: XCD e runs a contiguous range of the tile order, and that order walks
-  // group_m tile rows at a time, so the workgroups resident on one XCD share their X
-  // rows and weight rows in its L2. Any XCD count gives the same tiles.
+  // --- workgroup -> (K split, tile). Workgroups are dispatched round-robin over the
+  // XCDs, each with its own L2: XCD e runs a contiguous range of the work order (split
+  // major, then tiles), and the tile order walks group_m tile rows at a time, so the
+  // workgroups resident on one XCD share their X rows and weight rows in its L2. Any
+  // XCD count gives the same work items.
   const int ntiles = a.tiles_m * a.tiles_n;
+  const int nwork = ntiles * a.splits;
   const int xcd = blockIdx.x % kXcds, jx = blockIdx.x / kXcds;
-  const int t = xcd * (ntiles / kXcds) + min(xcd, ntiles % kXcds) + jx;
+  const int w_item = xcd * (nwork / kXcds) + min(xcd, nwork % kXcds) + jx;
+  const int ks = w_item / ntiles;
+  const int t = w_item - ks * ntiles;
   const int grp = t / (a.group_m * a.tiles_n), tg = t - grp * a.group_m * a.tiles_n;
   const int gm = min(a.group_m, a.tiles_m - grp * a.group_m);
   const int tile_m = grp * a.group_m + tg % gm;
   int tile_n = tg / gm;
   // --- tile -> (segment, first output column, first row) ---
-  int si = 0;
+  int si = 0, colbase = 0;  // colbase: columns of the segments before (partial sums)
   for (; si < a.nseg - 1; si++) {
     const int tn = (a.seg[si].n + OUT_BN - 1) / OUT_BN;
     if (tile_n < tn) break;
     tile_n -= tn;
+    colbase += a.seg[si].n;
   }
   const GemmSegment seg = a.seg[si];
   const int c0 = tile_n * OUT_BN;
@@ -323,17 +329,19 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
     mfmas(a1, b1);
   };
 
-  // Each k half runs nst_h stages [sb, sb + nst_h) of the K range (the last half fewer
-  // real ones). Main loop: straight-line bodies of NS stages (no branches between
+  // The workgroup's K split covers stages [kb, ke); each k half runs nst_h stages
+  // [sb, sb + nst_h) of it (the last half fewer real ones). Main loop: straight-line bodies of NS stages (no branches between
   // stages keeps the wait analysis per slot) over the stages that are active, full, and
   // prefetch no half stage; the rest go through the checked tail. Every half runs the
   // same number of stages, hence of barriers.
   using yes = std::true_type;
   using no = std::false_type;
-  const int nst_h = (nst + KSPLIT - 1) / KSPLIT;
+  const int kb = ks * a.split_stages;
+  const int ke = min(nst, kb + a.split_stages);
+  const int nst_h = (ke - kb + KSPLIT - 1) / KSPLIT;
   auto run = [&](auto H) __attribute__((always_inline)) {
-    const int sb = decltype(H)::value * nst_h;
-    const int se = min(nst, sb + nst_h);
+    const int sb = kb + decltype(H)::value * nst_h;
+    const int se = min(ke, sb + nst_h);
     static_for<kNS - 1>([&](auto J) { issue(H, J, sb + decltype(J)::value, yes{}); });
     int lim = se - sb;
     if (nb & 1) lim = min(lim, nst - kNS - sb);  // stage nst-NS prefetches the half stage
@@ -419,6 +427,18 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
                 old[r][f] + (float)(_Float16)acc[i][f][r];
         }
       }
+    } else if constexpr (EPI == EPI_PART) {
+      float *pb = a.part + (size_t)ks * a.m * a.ldp + colbase;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (row >= a.m) continue;
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+          const int col = c0 + wave * 32 * FN + 32 * f + l32;
+          if (col < seg.n) pb[(size_t)row * a.ldp + col] = acc[i][f][r];
+        }
+      }
     } else {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
@@ -438,6 +458,16 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
   }
 }
 
+// Splits of nst stages into equal runs with none empty: returns the split count and
+// the stages per split.
+int normalize_splits(int k, int splits, int *split_stages) {
+  const int nst = (k / 32 + 1) / 2;
+  splits = std::max(1, std::min(splits, nst));
+  const int per = (nst + splits - 1) / splits;
+  *split_stages = per;
+  return (nst + per - 1) / per;
+}
+
 template <int FM, int FN, int NS = 3, int KSPLIT = 1>
 int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   constexpr int BM = 32 * FM;
@@ -448,20 +478,24 @@ int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   for (int i = 0; i < a.nseg; i++) a.tiles_n += (a.seg[i].n + out_bn - 1) / out_bn;
   a.tiles_m = (a.m + BM - 1) / BM;
   a.group_m = 4;
-  const dim3 grid(a.tiles_m * a.tiles_n), block(256 * KSPLIT);
+  if (a.epi != EPI_PART || a.splits < 1) a.splits = 1;
+  a.splits = normalize_splits(a.k, a.splits, &a.split_stages);
+  const dim3 grid(a.tiles_m * a.tiles_n * a.splits), block(256 * KSPLIT);
   switch (a.epi) {
     case EPI_F16: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F16, KSPLIT>), grid, block, 0, s, a); break;
     case EPI_F32: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F32, KSPLIT>), grid, block, 0, s, a); break;
     case EPI_RESID: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_RESID, KSPLIT>), grid, block, 0, s, a); break;
     case EPI_SWIGLU: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_SWIGLU, KSPLIT>), grid, block, 0, s, a); break;
+    case EPI_PART: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_PART, KSPLIT>), grid, block, 0, s, a); break;
     default: return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "unknown GEMM epilogue");
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "gemm_q4_kernel launch");
 }
 
-// Compute units of the current device (cached per device).
-int cu_count() {
+}  // namespace
+
+int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -471,8 +505,6 @@ int cu_count() {
   }
   return cached[dev];
 }
-
-}  // namespace
 
 int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
   if (a.m <= 0) return SULIMO_HIP_OK;
@@ -498,7 +530,7 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
   int ntn = 0;
   const int out_bn = a.epi == EPI_SWIGLU ? 128 : 256;
   for (int i = 0; i < a.nseg; i++) ntn += (a.seg[i].n + out_bn - 1) / out_bn;
-  const int cus = cu_count();
+  const int cus = device_cu_count();
   const bool split = a.k >= 256 * 2;  // at least two 64-wide stages per half
   if (a.m <= 32) {
     if (split && ntn < 2 * cus) return launch_cfg<1, 2, 3, 2>(a, s);  // 32 x 256, K in halves

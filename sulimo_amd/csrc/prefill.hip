@@ -219,7 +219,7 @@ int32_t sulimo_hip_enqueue_attention_prefill(sulimo_hip_ctx *ctx, const sulimo_h
   a.n_head = (int)head_count;
   a.n_head_kv = (int)head_count_kv;
   a.head_dim = (int)head_dim;
-  if ((rc = ensure_workspace(ctx, attention_window_bytes(a)))) return rc;
+  if ((rc = ensure_workspace(ctx, attention_workspace_bytes(a)))) return rc;
   a.window = ctx->ws;
   wrote(out);
   return launch_attention(a, ctx->stream);
@@ -425,16 +425,18 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   const bool want_argmax = outputs && outputs->argmax_all;
   const bool own_logits = want_argmax && !outputs->logits_all;
   const size_t chunk_rows = 256;
-  // f16 copy of the attention key window (the same for every layer of the ubatch)
+  // attention workspace: f16 key window (the same for every layer of the ubatch) and
+  // split-key partial results
   AttnArgs probe_at{};
   probe_at.start_pos = (int)start_pos;
   probe_at.n = (int)n;
   probe_at.capacity = (int)cap;
+  probe_at.n_head = (int)Hq;
   probe_at.n_head_kv = (int)Hkv;
   probe_at.head_dim = (int)hd;
   const size_t off_w = off_l + ((own_logits ? chunk_rows * V * 4 : 0) + 255 & ~(size_t)255);
   // RoPE cos/sin table of the ubatch (shared by all layers)
-  const size_t off_r = off_w + (attention_window_bytes(probe_at) + 255 & ~(size_t)255);
+  const size_t off_r = off_w + (attention_workspace_bytes(probe_at) + 255 & ~(size_t)255);
   const size_t ws_need = off_r + n * (size_t)(cfg->rope_dim / 2) * 8;
   if ((rc = ensure_workspace(ctx, ws_need))) return rc;
   char *ws = reinterpret_cast<char *>(ctx->ws);

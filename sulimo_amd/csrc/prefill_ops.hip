@@ -253,6 +253,100 @@ __global__ __launch_bounds__(256) void rope_qkv_store_kernel(
   for (int i = lane; i < head_dim; i += 64) q8_block_store(buf[i], i & 31, dst + (i >> 5) * 34);
 }
 
+// Vector form of rope_qkv_store_kernel for rope_dim % 16 == 0: one thread per 8
+// consecutive elements ("unit") of one head slot of one token, 16-byte loads and
+// stores. A NeoX unit loads its 8 partner elements (rope_dim/2 away) as well; a Norm
+// unit holds its pairs. Same arithmetic as rope_qkv_store_kernel; a Q8_0 block is 4
+// neighbouring units (max over 4 lanes).
+__global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
+    _Float16 *q, const _Float16 *k, const _Float16 *v, int n_head, int n_head_kv, int head_dim,
+    int rope_dim, const float2 *cs_tab, int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
+    int slot0, int wrap) {
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  const int upw = head_dim / 8;  // units per head
+  const int slots = n_head + 2 * n_head_kv;
+  const long gid0 = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool valid = gid0 < (long)n * slots * upw;
+  const long gid = valid ? gid0 : 0;
+  const int u = (int)(gid % upw);
+  const long th = gid / upw;
+  const int hs = (int)(th % slots), t = (int)(th / slots);
+  const int half = rope_dim / 2;
+  const int kvd = n_head_kv * head_dim;
+  const int e0 = 8 * u;  // first element of the unit
+  const _Float16 *src;
+  if (hs < n_head) src = q + ((size_t)t * n_head + hs) * head_dim;
+  else if (hs < n_head + n_head_kv) src = k + (size_t)t * kvd + (size_t)(hs - n_head) * head_dim;
+  else src = v + (size_t)t * kvd + (size_t)(hs - n_head - n_head_kv) * head_dim;
+  const bool rot = hs < n_head + n_head_kv && e0 < rope_dim;
+  const bool lo = e0 < half;
+  const half8 xv = *reinterpret_cast<const half8 *>(src + e0);
+  half8 pv = xv;
+  if (rot && mode != 0) pv = *reinterpret_cast<const half8 *>(src + (lo ? e0 + half : e0 - half));
+  // q rotates in place and a NeoX partner unit belongs to another thread of the same
+  // workgroup (a head's units never straddle workgroups: 256 % (head_dim/8) == 0)
+  __syncthreads();
+  if (!valid) return;  // whole groups of 4 lanes exit together (head_dim/8 % 4 == 0)
+  float o[8];
+  if (rot) {
+    const float2 *cs = cs_tab + (size_t)t * half;
+    if (mode == 0) {  // pairs (2i, 2i+1) inside the unit
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const float2 r = cs[(e0 + j) / 2];
+        const float c = r.x, s = r.y;
+        const float v0 = (float)xv[j], v1 = (float)xv[j + 1];
+        o[j] = v0 * c - v1 * s;
+        o[j + 1] = v0 * s + v1 * c;
+      }
+    } else {  // pairs (i, i + half): the partner unit is half away
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float2 r = cs[(lo ? e0 : e0 - half) + j];
+        const float c = r.x, s = r.y;
+        if (lo) {
+          const float v0 = (float)xv[j], v1 = (float)pv[j];
+          o[j] = v0 * c - v1 * s;
+        } else {
+          const float v0 = (float)pv[j], v1 = (float)xv[j];
+          o[j] = v0 * s + v1 * c;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; j++) o[j] = (float)xv[j];
+  }
+  if (hs < n_head) {
+    half8 r;
+#pragma unroll
+    for (int j = 0; j < 8; j++) r[j] = (_Float16)o[j];
+    *reinterpret_cast<half8 *>(q + ((size_t)t * n_head + hs) * head_dim + e0) = r;
+    return;
+  }
+  // Q8_0 of block e0/32, held by the 4 lanes of units 4(u/4) .. +3
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; j++) amax = fmaxf(amax, fabsf(o[j]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  const bool is_k = hs < n_head + n_head_kv;
+  const int kvh = is_k ? hs - n_head : hs - n_head - n_head_kv;
+  const size_t row_bytes = (size_t)n_head_kv * (head_dim / 32) * 34;
+  const int row = (int)(((long)slot0 + t) % wrap);
+  uint8_t *blk = (is_k ? k_dst : v_dst) + (size_t)row * row_bytes + (size_t)kvh * (head_dim / 32) * 34 + (size_t)(u / 4) * 34;
+  if ((u & 3) == 0) *reinterpret_cast<_Float16 *>(blk) = (_Float16)d;
+  uint16_t *codes = reinterpret_cast<uint16_t *>(blk + 2 + 8 * (u & 3));  // 2-byte aligned
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    const float q0 = fminf(fmaxf(roundf(o[j] * id), -128.0f), 127.0f);
+    const float q1 = fminf(fmaxf(roundf(o[j + 1] * id), -128.0f), 127.0f);
+    codes[j / 2] = (uint16_t)((uint8_t)(int8_t)(int)q0 | ((uint16_t)(uint8_t)(int8_t)(int)q1 << 8));
+  }
+}
+
 __global__ void ring_commit_kernel(const uint16_t *src, uint16_t *ring, size_t row_u16, int slot0,
                                    int capacity, int n) {
   const int t = blockIdx.x;
@@ -411,6 +505,14 @@ int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v,
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "head_dim must be a multiple of 32 and <= 256");
   const size_t jobs = (size_t)n * (n_head + 2 * n_head_kv);
   if (jobs == 0) return SULIMO_HIP_OK;
+  if (rope_dim % 16 == 0 && 256 % (head_dim / 8) == 0) {
+    const size_t units = jobs * (size_t)(head_dim / 8);
+    hipLaunchKernelGGL(rope_qkv_store_vec_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<_Float16 *>(q), reinterpret_cast<const _Float16 *>(k),
+                       reinterpret_cast<const _Float16 *>(v), n_head, n_head_kv, head_dim, rope_dim,
+                       reinterpret_cast<const float2 *>(cs_tab), mode, n, k_dst, v_dst, slot0, wrap);
+    return check_launch("rope_qkv_store_vec_kernel");
+  }
   hipLaunchKernelGGL(rope_qkv_store_kernel, dim3(blocks_for(jobs, 4)), dim3(256), 0, s,
                      reinterpret_cast<_Float16 *>(q), reinterpret_cast<const _Float16 *>(k),
                      reinterpret_cast<const _Float16 *>(v), n_head, n_head_kv, head_dim, rope_dim,

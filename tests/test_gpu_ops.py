@@ -145,6 +145,11 @@ def _ring(rng, cap, hkv, hd):
     (6, 2, 128, 70, 0, 128),       # Llama grouping (3 q heads per kv head)
     (4, 4, 64, 40, 3, 64),         # MHA, head_dim 64
     (12, 2, 128, 50, 200, 128),    # window of the last `capacity` positions (ring wrap)
+    # long key ranges: query blocks split over several workgroups and merged
+    (12, 2, 128, 7, 1500, 2048),   # a few queries after a long context
+    (12, 2, 128, 1024, 0, 1024),   # long fresh prompt
+    (6, 2, 128, 300, 900, 1024),   # Llama grouping, resumed, near the window edge
+    (4, 4, 64, 200, 2000, 256),    # head_dim 64, ring wrap with split blocks
 ])
 def test_attention_prefill(ctx, hq, hkv, hd, n, start, cap):
     rng = np.random.default_rng(hq * 7 + n + start)
