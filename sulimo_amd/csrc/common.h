@@ -118,12 +118,19 @@ struct GemmArgs {
   int splits, split_stages;
   float *part;
   int ldp;
+  // Workspace launch_gemm_q4_0 may use for K-split partials (none when part is null).
+  size_t part_bytes;
   // Tile grid, filled by the launcher: tiles_m x tiles_n tiles, visited in groups of
   // group_m tile rows.
   int tiles_m, tiles_n, group_m;
 };
 
+// Runs X W^T with the tile configuration and K split a cost model picks for the shape;
+// a K split writes f32 partials to a.part (a.part_bytes) and reduces them in a second
+// kernel.
 int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s);
+// Partial-sum workspace launch_gemm_q4_0 would use for this GEMM given unlimited room.
+size_t gemm_q4_0_workspace_bytes(const GemmArgs &a);
 
 // Compute units of the current device (cached per device).
 int device_cu_count();

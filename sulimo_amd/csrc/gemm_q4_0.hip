@@ -458,6 +458,43 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
   }
 }
 
+// Sum of the K splits' partials in split order (deterministic), then the real epilogue:
+// one thread per 4 consecutive columns of the concatenated segment columns of a row.
+template <int EPI>
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs a) {
+  const int c4 = a.ldp / 4;
+  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (long)a.m * c4) return;
+  const int row = (int)(gid / c4);
+  int col = (int)(gid - (long)row * c4) * 4;
+  const size_t plane = (size_t)a.m * a.ldp;
+  const float *p = a.part + (size_t)row * a.ldp + col;
+  float4 v = *reinterpret_cast<const float4 *>(p);
+  for (int s = 1; s < a.splits; s++) {
+    const float4 w = *reinterpret_cast<const float4 *>(p + s * plane);
+    v.x += w.x;
+    v.y += w.y;
+    v.z += w.z;
+    v.w += w.w;
+  }
+  int si = 0;
+  while (si < a.nseg - 1 && col >= a.seg[si].n) col -= a.seg[si++].n;  // segment widths are multiples of 4
+  const GemmSegment seg = a.seg[si];
+  const size_t o = (size_t)row * seg.ldo + seg.col0 + col;
+  if constexpr (EPI == EPI_F16) {
+    typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<half4v *>(reinterpret_cast<_Float16 *>(seg.out) + o) =
+        half4v{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+  } else if constexpr (EPI == EPI_F32) {
+    *reinterpret_cast<float4 *>(reinterpret_cast<float *>(seg.out) + o) = v;
+  } else {  // EPI_RESID: x += f16(acc)
+    float4 *x = reinterpret_cast<float4 *>(reinterpret_cast<float *>(seg.out) + o);
+    const float4 old = *x;
+    *x = float4{old.x + (float)(_Float16)v.x, old.y + (float)(_Float16)v.y, old.z + (float)(_Float16)v.z,
+                old.w + (float)(_Float16)v.w};
+  }
+}
+
 // Splits of nst stages into equal runs with none empty: returns the split count and
 // the stages per split.
 int normalize_splits(int k, int splits, int *split_stages) {
@@ -506,11 +543,119 @@ int device_cu_count() {
   return cached[dev];
 }
 
+namespace {
+
+// Tile configurations the planner chooses from (all with 3 ring slots).
+enum GemmCfg : int { kT32, kT32K2, kT64, kT64K2, kT128, kNumCfg };
+constexpr int kCfgRows[kNumCfg] = {32, 32, 64, 64, 128};
+constexpr int kCfgKsplit[kNumCfg] = {1, 2, 1, 2, 1};
+
+// Cost model fitted to measurements on MI355X (clock ramped) of the layer shapes at
+// M = 128 .. 3071 (median error 7 %): per workgroup, fixed + stages x per-stage (us),
+// the per-stage cost rising when two workgroups share a CU; a floor of the operand
+// bytes every workgroup pulls into LDS over the chip's fetch rate; a K split adds the
+// reduction kernel.
+constexpr double kCostFixed[kNumCfg] = {2.92, 3.77, 5.01, 6.34, 9.15};
+constexpr double kCostStage[kNumCfg] = {0.495, 0.744, 0.552, 0.939, 0.811};
+constexpr double kCostShared[kNumCfg] = {0.012, 0.0, 0.179, 0.0, 0.464};
+constexpr double kFetchMBperUs = 8.65;
+constexpr double kReduceFixed = 5.09, kReducePerMB = 0.144;
+
+struct GemmPlan {
+  int cfg;
+  int splits;  // K splits across workgroups (1: the epilogue runs in the GEMM)
+};
+
+int seg_cols(const GemmArgs &a) {
+  int n = 0;
+  for (int i = 0; i < a.nseg; i++) n += a.seg[i].n;
+  return n;
+}
+
+double predict_us(const GemmArgs &a, int cfg, int splits, int cus) {
+  int per;
+  splits = normalize_splits(a.k, splits, &per);
+  const int out_bn = a.epi == EPI_SWIGLU ? 128 : 256;
+  long tn = 0;
+  for (int i = 0; i < a.nseg; i++) tn += (a.seg[i].n + out_bn - 1) / out_bn;
+  const long wgs = (long)(a.m + kCfgRows[cfg] - 1) / kCfgRows[cfg] * tn * splits;
+  const int stages = (per + kCfgKsplit[cfg] - 1) / kCfgKsplit[cfg];
+  const long load = (wgs + cus - 1) / cus;  // workgroups per CU
+  const int occ = kCfgKsplit[cfg] == 1 ? 2 : 1;
+  const long conc = std::min<long>(load, occ), seq = (load + occ - 1) / occ;
+  double t = seq * (kCostFixed[cfg] + stages * (kCostStage[cfg] + (conc - 1) * kCostShared[cfg]));
+  t = std::max(t, (double)wgs * per * (kCfgRows[cfg] * 128.0 + 9216.0) / 1e6 / kFetchMBperUs);
+  if (splits > 1) {
+    const double mn = (double)a.m * seg_cols(a);
+    const double out_bytes = a.epi == EPI_RESID ? 8 : a.epi == EPI_F32 ? 4 : 2;
+    t += kReduceFixed + kReducePerMB * (splits * mn * 4 + mn * out_bytes) / 1e6;
+  }
+  return t;
+}
+
+// A K split needs a splittable epilogue, 4-column aligned segments and room for the
+// partials (unless `unbounded`, used to size the workspace).
+bool can_split(const GemmArgs &a, int splits, bool unbounded) {
+  if (a.epi != EPI_F16 && a.epi != EPI_F32 && a.epi != EPI_RESID) return false;
+  for (int i = 0; i < a.nseg; i++)
+    if (a.seg[i].n % 4 || a.seg[i].ldo % 4 || a.seg[i].col0 % 4) return false;
+  if (unbounded) return true;
+  return a.part && (size_t)splits * a.m * seg_cols(a) * 4 <= a.part_bytes;
+}
+
+GemmPlan plan_gemm(const GemmArgs &a, bool unbounded) {
+  const int cus = device_cu_count();
+  if (a.epi == EPI_SWIGLU) {
+    // measured rule: 128 x 256 tiles once they fill the GPU four times over
+    int ntn = 0;
+    for (int i = 0; i < a.nseg; i++) ntn += (a.seg[i].n + 127) / 128;
+    const bool ks = a.k >= 512;
+    if (a.m <= 32) return {ks && ntn < 2 * cus ? kT32K2 : kT32, 1};
+    if (a.m > 64 && ntn * ((a.m + 127) / 128) >= 4 * cus) return {kT128, 1};
+    return {ks && ntn * ((a.m + 63) / 64) < 2 * cus ? kT64K2 : kT64, 1};
+  }
+  GemmPlan best1{kT64, 1}, bestn{kT64, 1};
+  double t1 = 1e30, tn = 1e30;
+  static const int kSplits[] = {1, 2, 3, 4, 6, 8};
+  for (int cfg = 0; cfg < kNumCfg; cfg++) {
+    if (kCfgKsplit[cfg] > 1 && a.k < 512) continue;  // at least two stages per half
+    if (kCfgRows[cfg] > 32 && a.m <= 32) continue;
+    for (int sp : kSplits) {
+      int per;
+      if (normalize_splits(a.k, sp, &per) != sp) continue;
+      if (sp > 1 && !can_split(a, sp, unbounded)) continue;
+      const double t = predict_us(a, cfg, sp, cus);
+      if (sp == 1 && t < t1) { t1 = t; best1 = {cfg, 1}; }
+      if (sp > 1 && t < tn) { tn = t; bestn = {cfg, sp}; }
+    }
+  }
+  return tn < 0.9 * t1 ? bestn : best1;  // split only for a clear predicted gain
+}
+
+int32_t launch_plan(const GemmArgs &a, int cfg, hipStream_t s) {
+  switch (cfg) {
+    case kT32: return launch_cfg<1, 2, 3, 1>(a, s);
+    case kT32K2: return launch_cfg<1, 2, 3, 2>(a, s);
+    case kT64: return launch_cfg<2, 2, 3, 1>(a, s);
+    case kT64K2: return launch_cfg<2, 2, 3, 2>(a, s);
+    default: return launch_cfg<4, 2, 3, 1>(a, s);
+  }
+}
+
+}  // namespace
+
+size_t gemm_q4_0_workspace_bytes(const GemmArgs &a) {
+  if (a.m <= 0 || a.k <= 0 || a.k % 32 != 0 || a.nseg < 1 || a.nseg > 3) return 0;
+  const GemmPlan p = plan_gemm(a, true);
+  return p.splits > 1 ? (size_t)p.splits * a.m * seg_cols(a) * 4 : 0;
+}
+
 int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
   if (a.m <= 0) return SULIMO_HIP_OK;
   if (a.k <= 0 || a.k % 32 != 0) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM k must be a positive multiple of 32");
   if (a.ldx < a.k) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM activation row stride below k");
   if (a.nseg < 1 || a.nseg > 3) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM needs 1..3 segments");
+  if (a.epi == EPI_PART) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM epilogue must be a final one");
   // Buffer offsets are 32-bit and stay below 2^31 (larger offsets mark rows past the end).
   const uint64_t lim = 1ull << 31;
   if ((uint64_t)a.m * (uint64_t)a.ldx * 2u >= lim)
@@ -523,23 +668,27 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
   }
   if (a.epi == EPI_SWIGLU && a.nseg != 1)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "SwiGLU GEMM takes one segment");
-  // Tile choice: each weight is dequantized once per workgroup and reused for BM rows,
-  // and two workgroups (or one of 8 waves) share a CU. 128 x 256 tiles move the fewest
-  // bytes per MAC but only pay off when they fill the GPU at least twice over. Grids
-  // smaller than two workgroups per CU split K inside the workgroup (8 waves).
-  int ntn = 0;
-  const int out_bn = a.epi == EPI_SWIGLU ? 128 : 256;
-  for (int i = 0; i < a.nseg; i++) ntn += (a.seg[i].n + out_bn - 1) / out_bn;
-  const int cus = device_cu_count();
-  const bool split = a.k >= 256 * 2;  // at least two 64-wide stages per half
-  if (a.m <= 32) {
-    if (split && ntn < 2 * cus) return launch_cfg<1, 2, 3, 2>(a, s);  // 32 x 256, K in halves
-    return launch_cfg<1, 2>(a, s);                                     // 32 x 256
+  const GemmPlan p = plan_gemm(a, false);
+  if (p.splits == 1) return launch_plan(a, p.cfg, s);
+  // K split: f32 partials per split, then their sum in split order with the epilogue
+  GemmArgs g = a;
+  g.epi = EPI_PART;
+  g.splits = p.splits;
+  g.ldp = seg_cols(a);
+  int32_t rc = launch_plan(g, p.cfg, s);
+  if (rc) return rc;
+  GemmArgs r = g;
+  r.epi = a.epi;
+  r.splits = normalize_splits(a.k, p.splits, &r.split_stages);
+  const long threads = (long)a.m * (r.ldp / 4);
+  const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+  switch (a.epi) {
+    case EPI_F16: hipLaunchKernelGGL(split_reduce_kernel<EPI_F16>, grid, block, 0, s, r); break;
+    case EPI_F32: hipLaunchKernelGGL(split_reduce_kernel<EPI_F32>, grid, block, 0, s, r); break;
+    default: hipLaunchKernelGGL(split_reduce_kernel<EPI_RESID>, grid, block, 0, s, r); break;
   }
-  const int tiles64 = ntn * ((a.m + 63) / 64);
-  if (a.m > 64 && ntn * ((a.m + 127) / 128) >= 4 * cus) return launch_cfg<4, 2>(a, s);  // 128 x 256
-  if (split && tiles64 < 2 * cus) return launch_cfg<2, 2, 3, 2>(a, s);                 // 64 x 256, K in halves
-  return launch_cfg<2, 2>(a, s);                                                       // 64 x 256
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "split_reduce_kernel launch");
 }
 
 }  // namespace sulimo

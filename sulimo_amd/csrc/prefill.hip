@@ -63,9 +63,11 @@ thread_local TokenBuf g_tok;
 
 // Y[n][m] = X[n][k] W[m][k]^T for the Q4_0 matrix W = (scales, quants), through its
 // panel copy (built on first use).
+// With own_workspace, a K split may use the context workspace for its partials (only
+// where no other data lives in it).
 int32_t gemm_plain(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
                    const sulimo_hip_buffer *quants, const void *x, void *out, size_t m, size_t k,
-                   size_t n, int epi) {
+                   size_t n, int epi, bool own_workspace = false) {
   const uint8_t *pan = nullptr;
   int32_t rc = get_q4_panels(ctx, scales, quants, nullptr, nullptr, (int)m, (int)k, &pan);
   if (rc) return rc;
@@ -77,6 +79,14 @@ int32_t gemm_plain(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
   a.epi = epi;
   a.seg[0] = GemmSegment{pan, out, (int)m, (int)m, 0};
   a.nseg = 1;
+  if (own_workspace) {
+    const size_t need = gemm_q4_0_workspace_bytes(a);
+    if (need) {
+      if ((rc = ensure_workspace(ctx, need))) return rc;
+      a.part = reinterpret_cast<float *>(ctx->ws);
+      a.part_bytes = need;
+    }
+  }
   return launch_gemm_q4_0(a, ctx->stream);
 }
 
@@ -126,7 +136,7 @@ int32_t sulimo_hip_enqueue_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_b
   NEED(out, n * m * 2, "out");
   if (n == 0) return SULIMO_HIP_OK;
   wrote(out);
-  return gemm_plain(ctx, scales, quants, x->dev, out->dev, m, k, n, EPI_F16);
+  return gemm_plain(ctx, scales, quants, x->dev, out->dev, m, k, n, EPI_F16, true);
 }
 
 int32_t sulimo_hip_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
@@ -437,10 +447,33 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   const size_t off_w = off_l + ((own_logits ? chunk_rows * V * 4 : 0) + 255 & ~(size_t)255);
   // RoPE cos/sin table of the ubatch (shared by all layers)
   const size_t off_r = off_w + (attention_workspace_bytes(probe_at) + 255 & ~(size_t)255);
-  const size_t ws_need = off_r + n * (size_t)(cfg->rope_dim / 2) * 8;
+  // K-split partials of the q/k/v, o and down GEMMs (sized by the GEMM planner)
+  const size_t off_g = off_r + (n * (size_t)(cfg->rope_dim / 2) * 8 + 255 & ~(size_t)255);
+  size_t gemm_ws = 0;
+  {
+    GemmArgs p{};
+    p.m = (int)n;
+    p.k = (int)D;
+    p.ldx = (int)D;
+    p.epi = EPI_F16;
+    p.seg[0] = GemmSegment{nullptr, nullptr, (int)qd, (int)qd, 0};
+    p.seg[1] = GemmSegment{nullptr, nullptr, (int)kvd, (int)kvd, 0};
+    p.seg[2] = GemmSegment{nullptr, nullptr, (int)kvd, (int)kvd, 0};
+    p.nseg = 3;
+    gemm_ws = std::max(gemm_ws, gemm_q4_0_workspace_bytes(p));
+    p.k = (int)qd;
+    p.epi = EPI_RESID;
+    p.seg[0] = GemmSegment{nullptr, nullptr, (int)D, (int)D, 0};
+    p.nseg = 1;
+    gemm_ws = std::max(gemm_ws, gemm_q4_0_workspace_bytes(p));
+    p.k = (int)F;
+    gemm_ws = std::max(gemm_ws, gemm_q4_0_workspace_bytes(p));
+  }
+  const size_t ws_need = off_g + gemm_ws;
   if ((rc = ensure_workspace(ctx, ws_need))) return rc;
   char *ws = reinterpret_cast<char *>(ctx->ws);
   float *xres = reinterpret_cast<float *>(ws);
+  float *gemm_part = reinterpret_cast<float *>(ws + off_g);
   uint8_t *stg_k = reinterpret_cast<uint8_t *>(ws + off_k);
   uint8_t *stg_v = reinterpret_cast<uint8_t *>(ws + off_v);
   hipStream_t s = ctx->stream;
@@ -494,6 +527,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     g.seg[1] = GemmSegment{pk, scratch->k->dev, (int)kvd, (int)kvd, 0};
     g.seg[2] = GemmSegment{pv, scratch->v->dev, (int)kvd, (int)kvd, 0};
     g.nseg = 3;
+    g.part = gemm_part;
+    g.part_bytes = gemm_ws;
     if ((rc = timed(ctx, PROF_GEMM, gemm_flop(g), gemm_bytes(g), [&] { return launch_gemm_q4_0(g, s); }))) return rc;
     // 3-4. RoPE on q and k, Q8_0 of k and v into the ring (or staging when wrapping)
     if ((rc = timed(ctx, PROF_ROPE_KV, 0, 2.0 * n * (qd + 2 * kvd) + 2.0 * n * qd + 2.0 * n * bpp, [&] {
@@ -542,6 +577,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     go.epi = EPI_RESID;
     go.seg[0] = GemmSegment{po, xres, (int)D, (int)D, 0};
     go.nseg = 1;
+    go.part = gemm_part;
+    go.part_bytes = gemm_ws;
     if ((rc = timed(ctx, PROF_GEMM, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s); }))) return rc;
     // 8. FFN RMSNorm
     if ((rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
@@ -568,6 +605,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     gd.epi = EPI_RESID;
     gd.seg[0] = GemmSegment{pd, xres, (int)D, (int)D, 0};
     gd.nseg = 1;
+    gd.part = gemm_part;
+    gd.part_bytes = gemm_ws;
     if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s); }))) return rc;
   }
   // 13. output RMSNorm of all n rows (h), final residual back to scratch.x as f16
