@@ -8,8 +8,11 @@ One step = device embedding gather of the 2048 prompt ids + execute_prefill_ubat
 (all 28 layers, final norm, LM head of the last token) ending in its blocking
 wait; weights, KV ring and scratch are resident in HBM before timing starts.
 
-Prints one JSON line. `value` is the rate of K timed steps with nothing else on the
-stream. `roofline` is the Q4_0 GEMM kernel (the dominant kernel), with its
+Prints one JSON line. Before the W warm-up steps, untimed steps run for at least
+half a second so that the GPU clock has left its idle state (counted under
+extra.prewarm). `value` is the rate of K timed steps with nothing else on the
+stream; extra.ubatch512 is the same prompt in the reference's default micro-batches
+of 512 tokens. `roofline` is the Q4_0 GEMM kernel (the dominant kernel), with its
 per-launch GPU time taken from hipEvents recorded around every launch over K more
 identical steps (the event records slow those steps, so they are kept out of
 `value`). `cpu_baseline` times the CPU oracle's restatement of the reference
@@ -33,6 +36,9 @@ PEAK_HBM_GBS = 8000.0
 SEED_MODEL = 0x5EED0002
 SEED_TOKENS = 0x5EED1002
 METRIC = "prefill tokens/s (Qwen2.5-1.5B Q4_0, 2048 tok)"
+
+
+PREWARM_S = 0.5
 
 
 def parse():
@@ -170,6 +176,13 @@ def main():
             dm.execute_prefill_ubatch(pos, m)
             pos += m
 
+    # The GPU clock ramps up from idle over a few hundred ms: untimed steps for at least
+    # PREWARM_S (counted in the output) before the W warm-up steps proper.
+    prewarm_steps, tp = 0, time.perf_counter()
+    while prewarm_steps == 0 or time.perf_counter() - tp < PREWARM_S:
+        step()
+        ctx.wait()
+        prewarm_steps += 1
     for _ in range(a.warmup):
         step()
     ctx.wait()
@@ -217,7 +230,26 @@ def main():
     extra = {"kernel_classes": {"gemm": cls(st.gemm), "attention": cls(st.attention), "norm": cls(st.norm),
                                 "rope_kv": cls(st.rope_kv)},
              "value_with_event_records": round(T * a.steps / wall_ev, 1),
+             "prewarm": {"steps": prewarm_steps, "min_seconds": PREWARM_S},
              "device": ctx.device_info.arch_name.decode()}
+    # The same prompt in the reference's default micro-batch of 512 tokens.
+    if a.ubatch != 512 and T > 512:
+        def step512():
+            for pos in range(0, T, 512):
+                m = min(512, T - pos)
+                dm.embed(tokens[pos:pos + m])
+                dm.execute_prefill_ubatch(pos, m)
+        for _ in range(a.warmup):
+            step512()
+        ctx.wait()
+        t2 = time.perf_counter()
+        for _ in range(a.steps):
+            step512()
+        ctx.wait()
+        w512 = time.perf_counter() - t2
+        extra["ubatch512"] = {"value": round(T * a.steps / w512, 1), "unit": "tokens/s",
+                              "ms_per_step": round(w512 / a.steps * 1e3, 3),
+                              "config": f"the {T}-token prompt in {-(-T // 512)} micro-batches of 512"}
     if not a.no_gemm:
         extra["gemm_shapes"] = gemm_table(ctx, hip, S)
     dm.release()

@@ -100,6 +100,37 @@ def test_resume_and_ring_wrap():
     dm.release()
 
 
+def test_llama_3b_layer_shapes():
+    """One layer of the Llama-3.2-3B shape (hidden 3072, FFN 8192, 24/8 heads, head_dim
+    128, Norm RoPE base 5e5; small vocab for the oracle's sake), prefilled in two chunks."""
+    cfg = S.ModelConfig(1, 3072, 8192, 24, 8, 128, 128, 2048, 500000.0, 1e-5, 0)
+    dm, okv, res = run_both(cfg, 55, [48, 40], 128)
+    for g, _, _, r in res:
+        assert np.max(np.abs(g - r)) <= 1e-2 * float(np.abs(r).max())
+        assert cosine(g, r) >= 0.999
+        assert int(np.argmax(g)) == int(np.argmax(r))
+    dk, dv = dm.kv_host()
+    assert kv_within_one_step(dk[0], okv.k[0], np.arange(88), dm.bpp)
+    assert kv_within_one_step(dv[0], okv.v[0], np.arange(88), dm.bpp)
+    dm.release()
+
+
+def test_resume_at_1536_with_wrap_at_2048():
+    """Edge-shape resume: 1536 positions written in ubatches of 512, then 1024 new tokens
+    appended to the capacity-2048 ring, wrapping at 2048 (the last ubatch's queries see
+    exactly the last 2048 positions)."""
+    cfg = TINY_NEOX
+    dm, okv, res = run_both(cfg, 66, [512, 512, 512, 1024], 2048)
+    for g, _, _, r in res:
+        assert np.max(np.abs(g - r)) <= 1e-2 * float(np.abs(r).max())
+        assert int(np.argmax(g)) == int(np.argmax(r))
+    dk, dv = dm.kv_host()
+    for l in range(cfg.n_layers):
+        assert kv_within_one_step(dk[l], okv.k[l], np.arange(2048), dm.bpp)
+        assert kv_within_one_step(dv[l], okv.v[l], np.arange(2048), dm.bpp)
+    dm.release()
+
+
 def test_all_positions_top1_agreement():
     """All-positions LM-head validation mode: device argmax per position equals the
     oracle's top-1 on >= 99.5 % of positions; logits within 1e-2 of their scale."""
