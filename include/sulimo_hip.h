@@ -213,6 +213,10 @@ typedef struct {
   sulimo_hip_buffer *ffn_gate_scales, *ffn_gate_quants;
   sulimo_hip_buffer *ffn_up_scales, *ffn_up_quants;
   sulimo_hip_buffer *ffn_down_scales, *ffn_down_quants;
+  /* Optional tensors of the CPU path (forward_pass.rs:250-272), NULL when absent;
+   * the reference's GPU path has none (prefill.rs:15-32): */
+  sulimo_hip_buffer *attn_q_bias, *attn_k_bias, *attn_v_bias; /* f32 [q_dim], [kv_dim], [kv_dim] */
+  sulimo_hip_buffer *attn_q_norm, *attn_k_norm;               /* f32 [head_dim] QK-norm weights */
 } sulimo_hip_layer_tensors;
 
 /* OclModelTensors (prefill.rs:35-40). */
@@ -247,7 +251,10 @@ typedef struct {
 /* execute_prefill_ubatch (prefill.rs:337-566): all layers of one micro-batch of n
  * tokens at positions start_pos.. on the context stream, then one blocking wait.
  * scratch.x must hold the n f16 token embeddings (sulimo_hip_embed_tokens or an
- * upload). Differences from the reference, all documented in the design notes:
+ * upload). Optional biases are added to the q/k/v GEMM results before their f16
+ * rounding, and the optional QK-norm (per-head RMSNorm, eps = cfg.eps) runs on q and
+ * k before RoPE, as forward_token does. Differences from the reference, all
+ * documented in the design notes:
  * the residual stream is kept in f32 between the kernels; when the ubatch wraps
  * the ring (start_pos+n > capacity), each query sees exactly the last `capacity`
  * positions (new K/V are staged and committed to the ring after attention). */

@@ -59,7 +59,8 @@ class OrcQ4(C.Structure):
 
 class OrcLayer(C.Structure):
     _fields_ = [("attn_norm", _P), ("q", OrcQ4), ("k", OrcQ4), ("v", OrcQ4), ("o", OrcQ4),
-                ("ffn_norm", _P), ("gate", OrcQ4), ("up", OrcQ4), ("down", OrcQ4)]
+                ("ffn_norm", _P), ("gate", OrcQ4), ("up", OrcQ4), ("down", OrcQ4),
+                ("q_bias", _P), ("k_bias", _P), ("v_bias", _P), ("q_norm", _P), ("k_norm", _P)]
 
 
 class OrcModel(C.Structure):
@@ -316,8 +317,9 @@ class OracleModel:
 
         layers = (OrcLayer * c.n_layers)()
         for i, L in enumerate(hm.layers):
+            opt = [None if a is None else _p(a) for a in (L.q_bias, L.k_bias, L.v_bias, L.q_norm, L.k_norm)]
             layers[i] = OrcLayer(_p(L.attn_norm), q4(L.q), q4(L.k), q4(L.v), q4(L.o),
-                                 _p(L.ffn_norm), q4(L.gate), q4(L.up), q4(L.down))
+                                 _p(L.ffn_norm), q4(L.gate), q4(L.up), q4(L.down), *opt)
         self._layers = layers
         self.model = OrcModel(self.cfg, q4(hm.token_embd), _p(hm.output_norm), q4(hm.output),
                               layers)

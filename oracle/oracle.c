@@ -486,6 +486,22 @@ void orc_lookup_token_embedding_f16(const uint8_t *scales, const uint8_t *quants
 
 static size_t kv_bpp(const orc_config *c) { return (size_t)c->n_head_kv * (c->head_dim / 32) * 34; }
 
+/* add_bias (forward_pass.rs:452-464) */
+static void add_bias(const float *b, float *v, size_t n) {
+  if (!b) return;
+  for (size_t i = 0; i < n; i++) v[i] += b[i];
+}
+
+/* apply_head_norms (forward_pass.rs:466-491): RMSNorm of every head with the shared
+ * [head_dim] weights (the non-Gemma form). */
+static void head_norms(const float *w, float *v, size_t heads, size_t hd, float eps, float *buf) {
+  if (!w) return;
+  for (size_t h = 0; h < heads; h++) {
+    memcpy(buf, v + h * hd, hd * 4);
+    orc_rmsnorm_scalar(buf, w, eps, hd, v + h * hd);
+  }
+}
+
 int orc_forward_token(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos, float *logits) {
   const orc_config *c = &m->cfg;
   size_t D = c->embd, F = c->ffn, hd = c->head_dim;
@@ -514,6 +530,11 @@ int orc_forward_token(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos
     orc_matvec_q4_0_q8_0_avx2(L->q.scales, L->q.quants, q8, qd, D, q);
     orc_matvec_q4_0_q8_0_avx2(L->k.scales, L->k.quants, q8, kvd, D, k);
     orc_matvec_q4_0_q8_0_avx2(L->v.scales, L->v.quants, q8, kvd, D, v);
+    add_bias(L->q_bias, q, qd);
+    add_bias(L->k_bias, k, kvd);
+    add_bias(L->v_bias, v, kvd);
+    head_norms(L->q_norm, q, c->n_head, hd, c->eps, deq);
+    head_norms(L->k_norm, k, c->n_head_kv, hd, c->eps, deq);
     for (int hh = 0; hh < c->n_head; hh++)
       orc_rope_head_scalar(q + hh * hd, pos, c->rope_dim, c->rope_base, c->rope_mode);
     for (int hh = 0; hh < c->n_head_kv; hh++)
@@ -556,9 +577,13 @@ static void round_f16_inplace(float *a, size_t n) {
 }
 
 /* GEMM with f16 input rounding and f16 output rounding, as gemm_q4_0_f16_scalar_reference
- * on f16 buffers (values kept as f32 holding exact f16 numbers). */
-static int gemm_f16io(orc_q4 w, const float *x16, size_t m, size_t k, size_t n, float *out) {
+ * on f16 buffers (values kept as f32 holding exact f16 numbers); an optional bias
+ * [m] is added before the output rounding. */
+static int gemm_f16io(orc_q4 w, const float *x16, size_t m, size_t k, size_t n, float *out,
+                      const float *bias) {
   if (gemm_q4_f32x(w.scales, w.quants, x16, m, k, n, out, m)) return -1;
+  if (bias)
+    for (size_t t = 0; t < n; t++) add_bias(bias, out + t * m, m);
   round_f16_inplace(out, n * m);
   return 0;
 }
@@ -583,11 +608,13 @@ int orc_prefill_reference(const orc_model *m, orc_kv *kv, const uint16_t *x_in, 
     const orc_layer *L = &m->layers[l];
     for (size_t t = 0; t < n; t++) orc_rmsnorm_scalar(x + t * D, L->attn_norm, c->eps, D, h + t * D);
     round_f16_inplace(h, n * D);
-    rc |= gemm_f16io(L->q, h, qd, D, n, q);
-    rc |= gemm_f16io(L->k, h, kvd, D, n, k);
-    rc |= gemm_f16io(L->v, h, kvd, D, n, v);
+    rc |= gemm_f16io(L->q, h, qd, D, n, q, L->q_bias);
+    rc |= gemm_f16io(L->k, h, kvd, D, n, k, L->k_bias);
+    rc |= gemm_f16io(L->v, h, kvd, D, n, v, L->v_bias);
     for (size_t t = 0; t < n; t++) {
       size_t pos = start_pos + t;
+      head_norms(L->q_norm, q + t * qd, c->n_head, hd, c->eps, t2);
+      head_norms(L->k_norm, k + t * kvd, c->n_head_kv, hd, c->eps, t2);
       for (int hh = 0; hh < c->n_head; hh++)
         orc_rope_head_scalar(q + t * qd + hh * hd, pos, c->rope_dim, c->rope_base, c->rope_mode);
       for (int hh = 0; hh < c->n_head_kv; hh++)
@@ -639,15 +666,15 @@ int orc_prefill_reference(const orc_model *m, orc_kv *kv, const uint16_t *x_in, 
       memcpy(kv->v[l] + ((start_pos + t) % cap) * bpp, nv + t * bpp, bpp);
     }
     round_f16_inplace(ao, n * qd);
-    rc |= gemm_f16io(L->o, ao, D, qd, n, t2);
+    rc |= gemm_f16io(L->o, ao, D, qd, n, t2, NULL);
     for (size_t i = 0; i < n * D; i++) x[i] += t2[i];
     for (size_t t = 0; t < n; t++) orc_rmsnorm_scalar(x + t * D, L->ffn_norm, c->eps, D, h + t * D);
     round_f16_inplace(h, n * D);
-    rc |= gemm_f16io(L->gate, h, F, D, n, g);
-    rc |= gemm_f16io(L->up, h, F, D, n, u);
+    rc |= gemm_f16io(L->gate, h, F, D, n, g, NULL);
+    rc |= gemm_f16io(L->up, h, F, D, n, u, NULL);
     orc_swiglu_scalar(g, u, n * F, g);
     round_f16_inplace(g, n * F);
-    rc |= gemm_f16io(L->down, g, D, F, n, t2);
+    rc |= gemm_f16io(L->down, g, D, F, n, t2, NULL);
     for (size_t i = 0; i < n * D; i++) x[i] += t2[i];
   }
   if (rc) goto done;

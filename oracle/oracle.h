@@ -118,6 +118,11 @@ typedef struct {
   orc_q4 q, k, v, o;
   const float *ffn_norm;
   orc_q4 gate, up, down;
+  /* optional (NULL when absent), forward_pass.rs:250-272: f32 q/k/v biases added to
+   * the projections, f32 [head_dim] RMSNorm weights applied per head of q and k
+   * before RoPE (apply_head_norms, forward_pass.rs:466-491) */
+  const float *q_bias, *k_bias, *v_bias;
+  const float *q_norm, *k_norm;
 } orc_layer;
 
 typedef struct {
@@ -136,7 +141,8 @@ typedef struct {
 } orc_kv;
 
 /* forward_token (crates/sulimo-engine/src/forward_pass.rs:190-417), Llama/Qwen2
- * graph without optional bias / QK-norm / post-norm tensors. Writes vocab logits.
+ * graph with the optional q/k/v biases and QK-norm (no post-norm tensors). Writes
+ * vocab logits.
  * Returns 0, or -1 when a scratch allocation fails. */
 int orc_forward_token(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos, float *logits);
 
@@ -145,6 +151,8 @@ int orc_forward_token(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos
  * reference's own CPU oracle (crates/sulimo-ocl/tests/test_prefill.rs:582-885):
  * f32 residual, f16 at every GEMM input and output, RoPE in f32, K quantized to
  * Q8_0 from the rotated f32 values, V from the f16 GEMM output, f32 attention.
+ * Optional biases are added to the f32 GEMM result before its f16 rounding; the
+ * optional QK-norm runs in f32 on the rounded q/k heads before RoPE.
  * x_in: f16 [n][embd] token embeddings. Attention is a sliding window of the
  * last `capacity` positions; new K/V are committed to the ring after attention.
  * logits: f32 [vocab] of token n-1, or [n][vocab] when all_logits != 0.

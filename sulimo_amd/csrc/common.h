@@ -104,6 +104,7 @@ struct GemmSegment {
   int n;
   int ldo;
   int col0;
+  const float *bias;  // optional f32 [n] added before the output rounding (F16/F32 epilogues)
 };
 
 struct GemmArgs {
@@ -171,10 +172,13 @@ int32_t launch_embed_q4_0(const uint16_t *scales, const uint8_t *quants, const u
 // cos/sin table of a ubatch for the fused RoPE: float2 [n][rope_dim/2] at positions
 // start_pos .. start_pos+n-1.
 int32_t launch_rope_table(float *tab, int rope_dim, float freq_base, int start_pos, int n, hipStream_t s);
+// q_norm / k_norm: optional f32 [head_dim] QK-norm weights (per-head RMSNorm with eps
+// before the rotation), or null.
 int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v, int n_head,
                               int n_head_kv, int head_dim, int rope_dim, const float *cs_tab,
                               int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
-                              int slot0, int wrap, hipStream_t s);
+                              int slot0, int wrap, const float *q_norm, const float *k_norm,
+                              float eps, hipStream_t s);
 // Copies n rows of `row_bytes` from src to ring slots (slot0 + t) % capacity.
 int32_t launch_ring_commit(const uint8_t *src, uint8_t *ring, size_t row_bytes, int slot0,
                            int capacity, int n, hipStream_t s);

@@ -449,7 +449,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
           const int col = c0 + wave * 32 * FN + 32 * f + l32;
           if (col >= seg.n) continue;
           const size_t o = (size_t)row * seg.ldo + seg.col0 + col;
-          const float v = acc[i][f][r];
+          const float v = acc[i][f][r] + (seg.bias ? seg.bias[col] : 0.0f);
           if constexpr (EPI == EPI_F16) reinterpret_cast<_Float16 *>(seg.out)[o] = (_Float16)v;
           else reinterpret_cast<float *>(seg.out)[o] = v;
         }
@@ -480,6 +480,13 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs a) {
   int si = 0;
   while (si < a.nseg - 1 && col >= a.seg[si].n) col -= a.seg[si++].n;  // segment widths are multiples of 4
   const GemmSegment seg = a.seg[si];
+  if (seg.bias) {
+    const float4 b = *reinterpret_cast<const float4 *>(seg.bias + col);
+    v.x += b.x;
+    v.y += b.y;
+    v.z += b.z;
+    v.w += b.w;
+  }
   const size_t o = (size_t)row * seg.ldo + seg.col0 + col;
   if constexpr (EPI == EPI_F16) {
     typedef _Float16 half4v __attribute__((ext_vector_type(4)));

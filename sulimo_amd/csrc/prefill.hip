@@ -90,6 +90,9 @@ int32_t gemm_plain(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
   return launch_gemm_q4_0(a, ctx->stream);
 }
 
+// Device pointer of an optional f32 tensor (null when absent).
+const float *opt_f32(const sulimo_hip_buffer *b) { return b ? reinterpret_cast<const float *>(b->dev) : nullptr; }
+
 // Runs one launch between profiling events (no-op events when profiling is off).
 template <typename F>
 int32_t timed(sulimo_hip_ctx *ctx, int cls, double flop, double bytes, F &&launch) {
@@ -421,6 +424,11 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     NEED(T.ffn_up_quants, F * nbD * 16, "ffn_up_quants");
     NEED(T.ffn_down_scales, D * nbF * 2, "ffn_down_scales");
     NEED(T.ffn_down_quants, D * nbF * 16, "ffn_down_quants");
+    if (T.attn_q_bias) NEED(T.attn_q_bias, qd * 4, "attn_q_bias");
+    if (T.attn_k_bias) NEED(T.attn_k_bias, kvd * 4, "attn_k_bias");
+    if (T.attn_v_bias) NEED(T.attn_v_bias, kvd * 4, "attn_v_bias");
+    if (T.attn_q_norm) NEED(T.attn_q_norm, hd * 4, "attn_q_norm");
+    if (T.attn_k_norm) NEED(T.attn_k_norm, hd * 4, "attn_k_norm");
     NEED(kv->k_buffers[l], cap * bpp, "kv k");
     NEED(kv->v_buffers[l], cap * bpp, "kv v");
   }
@@ -523,9 +531,9 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     g.k = (int)D;
     g.ldx = (int)D;
     g.epi = EPI_F16;
-    g.seg[0] = GemmSegment{pq, scratch->q->dev, (int)qd, (int)qd, 0};
-    g.seg[1] = GemmSegment{pk, scratch->k->dev, (int)kvd, (int)kvd, 0};
-    g.seg[2] = GemmSegment{pv, scratch->v->dev, (int)kvd, (int)kvd, 0};
+    g.seg[0] = GemmSegment{pq, scratch->q->dev, (int)qd, (int)qd, 0, opt_f32(T.attn_q_bias)};
+    g.seg[1] = GemmSegment{pk, scratch->k->dev, (int)kvd, (int)kvd, 0, opt_f32(T.attn_k_bias)};
+    g.seg[2] = GemmSegment{pv, scratch->v->dev, (int)kvd, (int)kvd, 0, opt_f32(T.attn_v_bias)};
     g.nseg = 3;
     g.part = gemm_part;
     g.part_bytes = gemm_ws;
@@ -536,7 +544,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
                                         dp<const uint16_t>(scratch->v), (int)Hq, (int)Hkv, (int)hd,
                                         cfg->rope_dim, rope_tab, cfg->rope_mode, in,
                                         staged ? stg_k : ring_k, staged ? stg_v : ring_v,
-                                        staged ? 0 : (int)(start_pos % cap), staged ? in : (int)cap, s);
+                                        staged ? 0 : (int)(start_pos % cap), staged ? in : (int)cap,
+                                        opt_f32(T.attn_q_norm), opt_f32(T.attn_k_norm), cfg->eps, s);
          })))
       return rc;
     // 5. causal GQA attention

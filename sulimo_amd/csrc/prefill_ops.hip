@@ -208,7 +208,7 @@ __global__ void embed_q4_kernel(const uint16_t *scales, const uint8_t *quants,
 __global__ __launch_bounds__(256) void rope_qkv_store_kernel(
     _Float16 *q, const _Float16 *k, const _Float16 *v, int n_head, int n_head_kv, int head_dim,
     int rope_dim, const float2 *cs_tab, int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
-    int slot0, int wrap) {
+    int slot0, int wrap, const float *q_norm, const float *k_norm, float eps) {
   __shared__ float sh[4][256];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int slots = n_head + 2 * n_head_kv;
@@ -227,6 +227,16 @@ __global__ __launch_bounds__(256) void rope_qkv_store_kernel(
       hp = const_cast<_Float16 *>(k) + (size_t)t * kvd + (size_t)(hs - n_head) * head_dim;
     for (int i = lane; i < head_dim; i += 64) buf[i] = (float)hp[i];
     __builtin_amdgcn_wave_barrier();
+    // optional QK-norm: RMSNorm of the head with the shared [head_dim] weights
+    const float *nw = hs < n_head ? q_norm : k_norm;
+    if (nw) {
+      float ss = 0.0f;
+      for (int i = lane; i < head_dim; i += 64) ss += buf[i] * buf[i];
+      ss = wave_sum(ss);
+      const float scale = 1.0f / sqrtf(ss / (float)head_dim + eps);
+      for (int i = lane; i < head_dim; i += 64) buf[i] = buf[i] * scale * nw[i];
+      __builtin_amdgcn_wave_barrier();
+    }
     for (int i = lane; i < half; i += 64) {
       const float2 cs = cs_tab[(size_t)t * half + i];
       const float c = cs.x, s = cs.y;
@@ -261,7 +271,7 @@ __global__ __launch_bounds__(256) void rope_qkv_store_kernel(
 __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
     _Float16 *q, const _Float16 *k, const _Float16 *v, int n_head, int n_head_kv, int head_dim,
     int rope_dim, const float2 *cs_tab, int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
-    int slot0, int wrap) {
+    int slot0, int wrap, const float *q_norm, const float *k_norm, float eps) {
   typedef _Float16 half8 __attribute__((ext_vector_type(8)));
   const int upw = head_dim / 8;  // units per head
   const int slots = n_head + 2 * n_head_kv;
@@ -286,7 +296,29 @@ __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
   // q rotates in place and a NeoX partner unit belongs to another thread of the same
   // workgroup (a head's units never straddle workgroups: 256 % (head_dim/8) == 0)
   __syncthreads();
-  if (!valid) return;  // whole groups of 4 lanes exit together (head_dim/8 % 4 == 0)
+  if (!valid) return;  // whole heads exit together (n * slots * head_dim/8 threads)
+  // optional QK-norm: RMSNorm of the head (its head_dim/8 consecutive lanes) with the
+  // shared [head_dim] weights, before the rotation; partner values use the same scale
+  float xf[8], pf[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    xf[j] = (float)xv[j];
+    pf[j] = (float)pv[j];
+  }
+  const float *nw = hs < n_head ? q_norm : hs < n_head + n_head_kv ? k_norm : nullptr;
+  if (nw) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) ss += xf[j] * xf[j];
+    for (int sh = upw / 2; sh >= 1; sh >>= 1) ss += __shfl_xor(ss, sh, 64);
+    const float scale = 1.0f / sqrtf(ss / (float)head_dim + eps);
+    const int pe0 = rot && mode != 0 ? (lo ? e0 + half : e0 - half) : e0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      xf[j] = xf[j] * scale * nw[e0 + j];
+      pf[j] = pf[j] * scale * nw[pe0 + j];
+    }
+  }
   float o[8];
   if (rot) {
     const float2 *cs = cs_tab + (size_t)t * half;
@@ -295,7 +327,7 @@ __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
       for (int j = 0; j < 8; j += 2) {
         const float2 r = cs[(e0 + j) / 2];
         const float c = r.x, s = r.y;
-        const float v0 = (float)xv[j], v1 = (float)xv[j + 1];
+        const float v0 = xf[j], v1 = xf[j + 1];
         o[j] = v0 * c - v1 * s;
         o[j + 1] = v0 * s + v1 * c;
       }
@@ -305,17 +337,17 @@ __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
         const float2 r = cs[(lo ? e0 : e0 - half) + j];
         const float c = r.x, s = r.y;
         if (lo) {
-          const float v0 = (float)xv[j], v1 = (float)pv[j];
+          const float v0 = xf[j], v1 = pf[j];
           o[j] = v0 * c - v1 * s;
         } else {
-          const float v0 = (float)pv[j], v1 = (float)xv[j];
+          const float v0 = pf[j], v1 = xf[j];
           o[j] = v0 * s + v1 * c;
         }
       }
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < 8; j++) o[j] = (float)xv[j];
+    for (int j = 0; j < 8; j++) o[j] = xf[j];
   }
   if (hs < n_head) {
     half8 r;
@@ -500,7 +532,8 @@ int32_t launch_rope_table(float *tab, int rope_dim, float freq_base, int start_p
 int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v, int n_head,
                               int n_head_kv, int head_dim, int rope_dim, const float *cs_tab,
                               int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
-                              int slot0, int wrap, hipStream_t s) {
+                              int slot0, int wrap, const float *q_norm, const float *k_norm,
+                              float eps, hipStream_t s) {
   if (head_dim > 256 || head_dim % 32 != 0)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "head_dim must be a multiple of 32 and <= 256");
   const size_t jobs = (size_t)n * (n_head + 2 * n_head_kv);
@@ -510,13 +543,15 @@ int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v,
     hipLaunchKernelGGL(rope_qkv_store_vec_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s,
                        reinterpret_cast<_Float16 *>(q), reinterpret_cast<const _Float16 *>(k),
                        reinterpret_cast<const _Float16 *>(v), n_head, n_head_kv, head_dim, rope_dim,
-                       reinterpret_cast<const float2 *>(cs_tab), mode, n, k_dst, v_dst, slot0, wrap);
+                       reinterpret_cast<const float2 *>(cs_tab), mode, n, k_dst, v_dst, slot0, wrap, q_norm,
+                       k_norm, eps);
     return check_launch("rope_qkv_store_vec_kernel");
   }
   hipLaunchKernelGGL(rope_qkv_store_kernel, dim3(blocks_for(jobs, 4)), dim3(256), 0, s,
                      reinterpret_cast<_Float16 *>(q), reinterpret_cast<const _Float16 *>(k),
                      reinterpret_cast<const _Float16 *>(v), n_head, n_head_kv, head_dim, rope_dim,
-                     reinterpret_cast<const float2 *>(cs_tab), mode, n, k_dst, v_dst, slot0, wrap);
+                     reinterpret_cast<const float2 *>(cs_tab), mode, n, k_dst, v_dst, slot0, wrap, q_norm, k_norm,
+                     eps);
   return check_launch("rope_qkv_store_kernel");
 }
 

@@ -100,7 +100,9 @@ class LayerTensorsC(C.Structure):
         "attn_norm", "attn_q_scales", "attn_q_quants", "attn_k_scales", "attn_k_quants",
         "attn_v_scales", "attn_v_quants", "attn_out_scales", "attn_out_quants", "ffn_norm",
         "ffn_gate_scales", "ffn_gate_quants", "ffn_up_scales", "ffn_up_quants",
-        "ffn_down_scales", "ffn_down_quants")]
+        "ffn_down_scales", "ffn_down_quants",
+        # optional (NULL when absent): q/k/v biases, QK-norm weights
+        "attn_q_bias", "attn_k_bias", "attn_v_bias", "attn_q_norm", "attn_k_norm")]
 
 
 class ModelTensorsC(C.Structure):
@@ -398,13 +400,19 @@ class DeviceModel:
             d = dict(attn_norm=HipBuffer.from_host(ctx, L.attn_norm, True), q=q4(L.q), k=q4(L.k), v=q4(L.v),
                      o=q4(L.o), ffn_norm=HipBuffer.from_host(ctx, L.ffn_norm, True), gate=q4(L.gate),
                      up=q4(L.up), down=q4(L.down))
+            opt = []
+            for name in ("q_bias", "k_bias", "v_bias", "q_norm", "k_norm"):
+                a = getattr(L, name, None)
+                if a is not None:
+                    d[name] = HipBuffer.from_host(ctx, a, True)
+                opt.append(d[name].handle if a is not None else None)
             self.layers.append(d)
             lt[i] = LayerTensorsC(d["attn_norm"].handle, d["q"].scales.handle, d["q"].quants.handle,
                                   d["k"].scales.handle, d["k"].quants.handle, d["v"].scales.handle,
                                   d["v"].quants.handle, d["o"].scales.handle, d["o"].quants.handle,
                                   d["ffn_norm"].handle, d["gate"].scales.handle, d["gate"].quants.handle,
                                   d["up"].scales.handle, d["up"].quants.handle, d["down"].scales.handle,
-                                  d["down"].quants.handle)
+                                  d["down"].quants.handle, *opt)
         self._lt = lt
         self.token_embd = q4(hm.token_embd)
         self.output = self.token_embd if hm.output is hm.token_embd else q4(hm.output)

@@ -90,6 +90,13 @@ class HostLayer:
     gate: Q4Tensor
     up: Q4Tensor
     down: Q4Tensor
+    # Optional tensors of the CPU path (forward_pass.rs:250-272): f32 q/k/v biases
+    # (Qwen2) and per-head RMSNorm weights of q and k (QK-norm), None when absent.
+    q_bias: np.ndarray | None = None
+    k_bias: np.ndarray | None = None
+    v_bias: np.ndarray | None = None
+    q_norm: np.ndarray | None = None
+    k_norm: np.ndarray | None = None
 
 
 @dataclass
@@ -105,10 +112,13 @@ def _norm(rng, n):
     return (1.0 + rng.normal(0.0, 0.02, size=n)).astype(np.float32)
 
 
-def make_model(cfg: ModelConfig, seed: int, tie_embeddings: bool = True) -> HostModel:
+def make_model(cfg: ModelConfig, seed: int, tie_embeddings: bool = True, biases: bool = False,
+               qk_norm: bool = False) -> HostModel:
     """Random-init model. With tie_embeddings the LM head is token_embd (Qwen2.5
     ties them; the engine falls back to token_embd when output.weight is absent,
-    crates/sulimo-engine/src/forward_pass.rs:58)."""
+    crates/sulimo-engine/src/forward_pass.rs:58). biases adds q/k/v biases ~N(0, 0.5)
+    and qk_norm per-head norm weights ~1+N(0, 0.1), from their own seed stream (the
+    other tensors are the same as without them)."""
     ss = np.random.SeedSequence(seed)
     kids = iter(ss.spawn(4 + 9 * cfg.n_layers))
     rng = lambda: np.random.default_rng(next(kids))  # noqa: E731
@@ -123,6 +133,16 @@ def make_model(cfg: ModelConfig, seed: int, tie_embeddings: bool = True) -> Host
             attn_norm=_norm(rng(), D), q=random_q4(rng(), cfg.q_dim, D), k=random_q4(rng(), cfg.kv_dim, D),
             v=random_q4(rng(), cfg.kv_dim, D), o=random_q4(rng(), D, cfg.q_dim), ffn_norm=_norm(rng(), D),
             gate=random_q4(rng(), F, D), up=random_q4(rng(), F, D), down=random_q4(rng(), D, F)))
+    if biases or qk_norm:
+        er = np.random.default_rng(np.random.SeedSequence([seed, 0xB1A5]))
+        for L in layers:
+            if biases:
+                L.q_bias = er.normal(0.0, 0.5, cfg.q_dim).astype(np.float32)
+                L.k_bias = er.normal(0.0, 0.5, cfg.kv_dim).astype(np.float32)
+                L.v_bias = er.normal(0.0, 0.5, cfg.kv_dim).astype(np.float32)
+            if qk_norm:
+                L.q_norm = (1.0 + er.normal(0.0, 0.1, cfg.head_dim)).astype(np.float32)
+                L.k_norm = (1.0 + er.normal(0.0, 0.1, cfg.head_dim)).astype(np.float32)
     return HostModel(cfg, token_embd, output_norm, output, layers)
 
 

@@ -38,3 +38,24 @@ def test_errors_without_device_are_reported():
     with pytest.raises(hip.HipError) as e:
         hip.HipContext.get_or_init(0)
     assert e.value.code == hip.ERR_DEVICE_NOT_FOUND
+
+
+def _header_struct_fields(name):
+    """Member names of `typedef struct { ... } name;` in include/sulimo_hip.h."""
+    import re
+    from pathlib import Path
+    text = (Path(hip.LIB_PATH).parent.parent / "include" / "sulimo_hip.h").read_text()
+    body = re.search(r"typedef struct \{([^}]*)\}\s*" + name + r";", text).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for decl in body.split(";"):
+        if decl.strip():
+            fields += [re.findall(r"\w+", part)[-1] for part in decl.split(",")]
+    return fields
+
+
+@pytest.mark.parametrize("cname,cls", [("sulimo_hip_layer_tensors", "LayerTensorsC"),
+                                       ("sulimo_hip_prefill_scratch", "PrefillScratchC")])
+def test_ctypes_structs_match_header(cname, cls):
+    names = [f[0] for f in getattr(hip, cls)._fields_]
+    assert names == _header_struct_fields(cname)

@@ -40,10 +40,10 @@ def kv_within_one_step(dev_ring, ref_ring, slots, bpp):
     return bool(np.all(np.abs(cg * dg - cr * dr) <= bound))
 
 
-def run_both(cfg, seed, chunks, cap, all_logits=False):
+def run_both(cfg, seed, chunks, cap, all_logits=False, **model_kw):
     """Prefill the same token stream in `chunks` micro-batches on the GPU and in the oracle."""
     ctx = hip.HipContext.get_or_init(0)
-    hm = S.make_model(cfg, seed)
+    hm = S.make_model(cfg, seed, **model_kw)
     n_total = sum(chunks)
     toks = S.random_tokens(seed + 1, n_total, cfg.vocab)
     dm = hip.DeviceModel(ctx, hm, cap, max(chunks))
@@ -83,6 +83,27 @@ def test_tiny_prefill_matches_oracle(cfg):
         assert kv_within_one_step(dk[l], okv.k[l], np.arange(16), dm.bpp)
         assert kv_within_one_step(dv[l], okv.v[l], np.arange(16), dm.bpp)
     dm.release()
+
+
+@pytest.mark.parametrize("cfg", [TINY_NEOX, TINY_NORM, S.ModelConfig(2, 256, 512, 4, 2, 64, 40, 512, 10000.0, 1e-6, 1)],
+                         ids=["neox", "norm", "neox_rope40"])
+def test_bias_and_qk_norm(cfg):
+    """Optional q/k/v biases and QK-norm (forward_pass.rs:250-272): added to the GEMM
+    output before its f16 rounding, per-head RMSNorm before RoPE; matches the oracle
+    in two chunks and differs from the same model without them."""
+    dm, okv, res = run_both(cfg, 27, [16, 12], 64, biases=True, qk_norm=True)
+    for g, _, _, r in res:
+        scale = float(np.abs(r).max())
+        assert np.max(np.abs(g - r)) <= 1e-2 * scale
+        assert cosine(g, r) >= 0.999
+        assert int(np.argmax(g)) == int(np.argmax(r))
+    dk, dv = dm.kv_host()
+    for l in range(cfg.n_layers):
+        assert kv_within_one_step(dk[l], okv.k[l], np.arange(28), dm.bpp)
+        assert kv_within_one_step(dv[l], okv.v[l], np.arange(28), dm.bpp)
+    dm.release()
+    _, _, plain = run_both(cfg, 27, [16, 12], 64)
+    assert np.max(np.abs(plain[-1][0] - res[-1][0])) > 0.05 * float(np.abs(res[-1][3]).max())
 
 
 def test_resume_and_ring_wrap():

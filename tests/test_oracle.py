@@ -270,11 +270,21 @@ def _textbook_prefill(hm, x16, n):
         v[..., a], v[..., b] = va * cs - vb * sn, va * sn + vb * cs
         return v.reshape(n, nh * hd)
 
+    def proj(h, w, b):
+        y = h @ w.dequant_f32().T.astype(np.float64)
+        return y if b is None else y + b
+
+    def head_norm(v, w, nh):
+        if w is None:
+            return v
+        v = v.reshape(n * nh, hd)
+        return (v / np.sqrt(np.mean(v * v, axis=1, keepdims=True) + c.eps) * w).reshape(n, nh * hd)
+
     for L in hm.layers:
         h = rms(x, L.attn_norm)
-        q = rope(h @ L.q.dequant_f32().T.astype(np.float64), c.n_head)
-        k = rope(h @ L.k.dequant_f32().T.astype(np.float64), c.n_head_kv)
-        v = h @ L.v.dequant_f32().T.astype(np.float64)
+        q = rope(head_norm(proj(h, L.q, L.q_bias), L.q_norm, c.n_head), c.n_head)
+        k = rope(head_norm(proj(h, L.k, L.k_bias), L.k_norm, c.n_head_kv), c.n_head_kv)
+        v = proj(h, L.v, L.v_bias)
         k = oracle.dequant_q8_0(oracle.quantize_f32_to_q8_0(k.astype(np.float32))).reshape(n, -1)
         v = oracle.dequant_q8_0(oracle.quantize_f32_to_q8_0(v.astype(np.float32))).reshape(n, -1)
         ao = np.zeros((n, c.n_head * hd))
@@ -294,23 +304,29 @@ def _textbook_prefill(hm, x16, n):
     return h @ hm.output.dequant_f32().T.astype(np.float64)
 
 
+@pytest.mark.parametrize("extras", [False, True], ids=["plain", "bias_qknorm"])
 @pytest.mark.parametrize("mode", [0, 1])
-def test_prefill_reference_vs_textbook(mode):
+def test_prefill_reference_vs_textbook(mode, extras):
     cfg = S.ModelConfig(2, 128, 256, 4, 2, 32, 32, 96, 10000.0, 1e-6, mode)
-    hm = S.make_model(cfg, 3)
+    hm = S.make_model(cfg, 3, biases=extras, qk_norm=extras)
     toks = S.random_tokens(4, 12, cfg.vocab)
     x = S.embed_host(hm, toks)
     lg = oracle.prefill_reference(oracle.OracleModel(hm), oracle.OracleKv(cfg, 32), x, 0, all_logits=True)
     ref = _textbook_prefill(hm, x, 12)
     assert np.max(np.abs(lg - ref)) <= 2e-2 * np.abs(ref).max()
     assert np.mean(np.argmax(lg, 1) == np.argmax(ref, 1)) >= 0.9
+    if extras:  # the optional tensors change the result (they are not silently skipped)
+        plain = oracle.prefill_reference(oracle.OracleModel(S.make_model(cfg, 3)), oracle.OracleKv(cfg, 32), x, 0,
+                                         all_logits=True)
+        assert np.max(np.abs(plain - lg)) > 0.1 * np.abs(ref).max()
 
 
-def test_forward_token_vs_prefill_reference():
+@pytest.mark.parametrize("extras", [False, True], ids=["plain", "bias_qknorm"])
+def test_forward_token_vs_prefill_reference(extras):
     """forward_token (Q8_0 activations, AVX2 integer dots) tracks the fp16-activation
     prefill: logits cosine >= 0.99 and equal argmax (test_prefill.rs:863-885 gates)."""
     cfg = S.ModelConfig(2, 128, 256, 4, 2, 32, 32, 64, 10000.0, 1e-6, 1)
-    hm = S.make_model(cfg, 1)
+    hm = S.make_model(cfg, 1, biases=extras, qk_norm=extras)
     om = oracle.OracleModel(hm)
     toks = S.random_tokens(2, 16, cfg.vocab)
     lg = oracle.prefill_reference(om, oracle.OracleKv(cfg, 64), S.embed_host(hm, toks), 0, all_logits=True)
