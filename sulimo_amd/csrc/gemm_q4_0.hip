@@ -502,6 +502,122 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs a) {
   }
 }
 
+// GEMV for MT <= 4 tokens (decode, the last-token LM head): HBM-bound, so no MFMA and
+// no LDS staging of the weights. One wave per 32-row panel reads the panel's records
+// (lane l: quant bytes at 16*l, its row's two scales) U stages at a time, dequantizes
+// with the GEMM's f16 rounding and accumulates f16 x f16 products in f32
+// (v_dot2_f32_f16) against x held in LDS; the two half-waves of a row combine at the
+// end. x beyond K is zero in LDS, so the odd-block half stage adds nothing.
+constexpr int kGemvMaxXBytes = 64 * 1024;
+
+template <int MT, int EPI>
+__global__ __launch_bounds__(256) void gemv_q4_kernel(GemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 xs[];  // [MT][kpad]
+  constexpr int U = 8;  // stages in flight per wave
+  const int nb = a.k >> 5, nst = (nb + 1) >> 1, kpad = nst * 64;
+  for (int i = threadIdx.x; i < MT * kpad / 8; i += blockDim.x) {
+    const int t = i / (kpad / 8), c = (i % (kpad / 8)) * 8;
+    half8 v = half8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (t < a.m && c < a.k) v = *reinterpret_cast<const half8 *>(a.x + (size_t)t * a.ldx + c);  // k % 32 == 0
+    *reinterpret_cast<half8 *>(xs + t * kpad + c) = v;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+  int p = blockIdx.x * 4 + (threadIdx.x >> 6);  // panel across the segments
+  int si = 0;
+  for (; si < a.nseg; si++) {
+    const int np = (a.seg[si].n + 31) / 32;
+    if (p < np) break;
+    p -= np;
+  }
+  if (si >= a.nseg) return;  // whole waves past the last panel (no barrier below)
+  const GemmSegment seg = a.seg[si];
+  const uint8_t *rec0 = seg.panels + (size_t)p * nst * kQ4PanelRecord;
+  float acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++) acc[t] = 0.0f;
+  for (int s0 = 0; s0 < nst; s0 += U) {
+    uint4 qv[U];
+    uint32_t sw[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int st = min(s0 + u, nst - 1);  // repeats the last stage, not used below
+      qv[u] = *reinterpret_cast<const uint4 *>(rec0 + (size_t)st * kQ4PanelRecord + 16 * lane);
+      sw[u] = *reinterpret_cast<const uint32_t *>(rec0 + (size_t)st * kQ4PanelRecord + 1024 + 4 * r);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      if (s0 + u >= nst) break;
+      const int kb = (s0 + u) * 64;
+#pragma unroll
+      for (int b = 0; b < 2; b++) {
+        const uint32_t lo = b ? qv[u].z : qv[u].x, hi = b ? qv[u].w : qv[u].y;
+        const half2v d2 = as_h2(__builtin_amdgcn_perm(sw[u], sw[u], b ? 0x03020302u : 0x01000100u));
+        half2v w[8];  // elements 8h .. 8h+7, then 16+8h .. 16+8h+7 of block b
+        dq4<false>(lo & 0x0F0F0F0Fu, d2, w[0], w[1]);
+        dq4<false>(hi & 0x0F0F0F0Fu, d2, w[2], w[3]);
+        dq4<true>(lo & 0xF0F0F0F0u, d2, w[4], w[5]);
+        dq4<true>(hi & 0xF0F0F0F0u, d2, w[6], w[7]);
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+          const _Float16 *xr = xs + t * kpad + kb + 32 * b + 8 * h;
+          const half8 xl = *reinterpret_cast<const half8 *>(xr);
+          const half8 xh = *reinterpret_cast<const half8 *>(xr + 16);
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            acc[t] = __builtin_amdgcn_fdot2(w[j], half2v{xl[2 * j], xl[2 * j + 1]}, acc[t], false);
+            acc[t] = __builtin_amdgcn_fdot2(w[4 + j], half2v{xh[2 * j], xh[2 * j + 1]}, acc[t], false);
+          }
+        }
+      }
+    }
+  }
+  const int row = p * 32 + r;
+#pragma unroll
+  for (int t = 0; t < MT; t++) {
+    float v = acc[t] + __shfl_xor(acc[t], 32, 64);
+    if (h || t >= a.m || row >= seg.n) continue;
+    if (seg.bias) v += seg.bias[row];
+    const size_t o = (size_t)t * seg.ldo + seg.col0 + row;
+    if constexpr (EPI == EPI_F16) reinterpret_cast<_Float16 *>(seg.out)[o] = (_Float16)v;
+    else if constexpr (EPI == EPI_F32) reinterpret_cast<float *>(seg.out)[o] = v;
+    else {  // EPI_RESID
+      float *x = reinterpret_cast<float *>(seg.out) + o;
+      *x = *x + (float)(_Float16)v;
+    }
+  }
+}
+
+template <int MT>
+int32_t launch_gemv_mt(const GemmArgs &a, hipStream_t s) {
+  int panels = 0;
+  for (int i = 0; i < a.nseg; i++) panels += (a.seg[i].n + 31) / 32;
+  const int kpad = ((a.k / 32 + 1) / 2) * 64;
+  const size_t lds = (size_t)MT * kpad * 2;
+  const dim3 grid((unsigned)((panels + 3) / 4)), block(256);
+  switch (a.epi) {
+    case EPI_F16: hipLaunchKernelGGL((gemv_q4_kernel<MT, EPI_F16>), grid, block, lds, s, a); break;
+    case EPI_F32: hipLaunchKernelGGL((gemv_q4_kernel<MT, EPI_F32>), grid, block, lds, s, a); break;
+    default: hipLaunchKernelGGL((gemv_q4_kernel<MT, EPI_RESID>), grid, block, lds, s, a); break;
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "gemv_q4_kernel launch");
+}
+
+// The GEMV handles up to 4 tokens with f16/f32/residual epilogues and x in 64 KB of LDS.
+int gemv_tokens(int m) { return m == 1 ? 1 : m == 2 ? 2 : 4; }
+bool gemv_fits(const GemmArgs &a) {
+  const int kpad = ((a.k / 32 + 1) / 2) * 64;
+  return a.m <= 4 && (a.epi == EPI_F16 || a.epi == EPI_F32 || a.epi == EPI_RESID) &&
+         (size_t)gemv_tokens(a.m) * kpad * 2 <= (size_t)kGemvMaxXBytes && a.ldx % 8 == 0;
+}
+
+int32_t launch_gemv(const GemmArgs &a, hipStream_t s) {
+  if (a.m == 1) return launch_gemv_mt<1>(a, s);
+  if (a.m == 2) return launch_gemv_mt<2>(a, s);
+  return launch_gemv_mt<4>(a, s);
+}
+
 // Splits of nst stages into equal runs with none empty: returns the split count and
 // the stages per split.
 int normalize_splits(int k, int splits, int *split_stages) {
@@ -653,6 +769,7 @@ int32_t launch_plan(const GemmArgs &a, int cfg, hipStream_t s) {
 
 size_t gemm_q4_0_workspace_bytes(const GemmArgs &a) {
   if (a.m <= 0 || a.k <= 0 || a.k % 32 != 0 || a.nseg < 1 || a.nseg > 3) return 0;
+  if (gemv_fits(a)) return 0;
   const GemmPlan p = plan_gemm(a, true);
   return p.splits > 1 ? (size_t)p.splits * a.m * seg_cols(a) * 4 : 0;
 }
@@ -675,6 +792,7 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
   }
   if (a.epi == EPI_SWIGLU && a.nseg != 1)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "SwiGLU GEMM takes one segment");
+  if (gemv_fits(a)) return launch_gemv(a, s);
   const GemmPlan p = plan_gemm(a, false);
   if (p.splits == 1) return launch_plan(a, p.cfg, s);
   // K split: f32 partials per split, then their sum in split order with the epilogue

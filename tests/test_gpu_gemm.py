@@ -120,6 +120,37 @@ def test_odd_block_counts_and_ragged_rows(ctx, n_tok, k, m_out):
     assert max_rel_err(y, x.astype(np.float32) @ w.dequant_f32().T) <= 1e-2
 
 
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("k,m_out", [(800, 72), (1536, 256), (96, 40)])
+def test_gemv_small_m(ctx, M, k, m_out):
+    """Up to 4 tokens take the GEMV (no MFMA): odd block counts and ragged rows against
+    the oracle's scalar reference with the f16-weight error model, and fp32 within 1e-2."""
+    rng = np.random.default_rng(9000 + M * 7 + k + m_out)
+    w = S.random_q4(rng, m_out, k)
+    x = rng.standard_normal((M, k)).astype(np.float16)
+    y = run_gemm(ctx, w.scales, w.quants, x, m_out, k, M)
+    ref = oracle.gemm_q4_0_f16_scalar_reference(w.scales, w.quants, x, m_out, k, M)
+    err = np.abs(y.astype(np.float64) - ref.astype(np.float64))
+    assert np.all(err <= f16_weight_bound(x, w.scales, w.quants, ref))
+    assert max_rel_err(y, x.astype(np.float32) @ w.dequant_f32().T) <= 1e-2
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_gemv_one_hot_bit_exact(ctx, M):
+    """GEMV dequant is bit-exact: token t = e_(3t+1) reads column 3t+1 of W^T exactly."""
+    rng = np.random.default_rng(31 + M)
+    m_out, k = 96, 160
+    w = S.random_q4(rng, m_out, k)
+    w.quants.reshape(-1, 16)[:16] = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    x = np.zeros((M, k), np.float16)
+    cols = [3 * t + 1 for t in range(M)]
+    for t, c in enumerate(cols):
+        x[t, c] = 1.0
+    y = run_gemm(ctx, w.scales, w.quants, x, m_out, k, M)
+    deq = oracle.dequant_q4_0_soa(w.scales, w.quants).reshape(m_out, k)
+    assert np.array_equal(y.view(np.uint16), deq[:, cols].T.astype(np.float16).view(np.uint16))
+
+
 def test_panel_copy_follows_uploads(ctx):
     """The GEMM reads a panel copy of the weights built from the SoA buffers on first
     use; overwriting the buffers must be seen by the next GEMM (bit-exact one-hot
