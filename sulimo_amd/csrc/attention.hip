@@ -77,13 +77,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 __device__ __forceinline__ void wait_vmcnt0() { wait_vmcnt<0>(); }
 
-// Key steps of query block qblk (64-key tiles, two per step: one per half).
-__host__ __device__ inline int attn_block_steps(int qblk, int PB, int n, int start_pos, int cap, int wlo) {
+// Key steps of query block qblk (64-key tiles, one per half and step).
+__host__ __device__ inline int attn_block_steps(int qblk, int PB, int n, int start_pos, int cap, int wlo,
+                                                int halves) {
   const int tg0 = qblk * PB * 32;
   const int tg_last = (tg0 + PB * 32 < n ? tg0 + PB * 32 : n) - 1;
   const int jlo0 = start_pos + tg0 - cap + 1 - wlo;
   const int jlo = jlo0 > 0 ? jlo0 : 0, jhi = start_pos + tg_last - wlo;
-  return (jhi / kKT - jlo / kKT + 2) / 2;
+  return (jhi / kKT - jlo / kKT + halves) / halves;
 }
 __host__ __device__ inline int attn_pieces(int steps, int C) { return (steps + C - 1) / C; }
 
@@ -160,15 +161,15 @@ __global__ __launch_bounds__(256) void kv_window_kernel(AttnArgs a, long wlo, in
 // ---------------------------------------------------------------------------
 // 2. flash attention over the f16 window
 // ---------------------------------------------------------------------------
-// Split-key partial of one piece: per field, 256 floats (query wave x lane):
-// fields 0 .. 16*OT-1 = the O^T accumulator registers, then m, then the lane's l.
+// Split-key partial of one piece, per (query wave x lane) = 256 entries: the normalized
+// O^T registers O/l as f16 (16*OT fields of 256 f16), then m and the query's l as f32.
 template <int HD>
-constexpr int part_fields() { return 16 * (HD / 32) + 2; }
+constexpr int part_rec_floats() { return 16 * (HD / 32) * 128 + 2 * 256; }
 
-template <int HD>
-__global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo, int wpad, int HG, int PB,
-                                                            int n_qblk, int n_hgrp, int C, float *part,
-                                                            int pmax) {
+template <int HD, int H2>
+__global__ __launch_bounds__(256 * H2, 2 / H2) void flash_attn_kernel(AttnArgs a, long wlo, int wpad, int HG,
+                                                                      int PB, int n_qblk, int n_hgrp, int C,
+                                                                      float *part, int pmax) {
   constexpr int KS = HD / 16;          // S^T k-steps over head_dim
   constexpr int OT = HD / 32;          // O^T tiles over head_dim
   constexpr int KCH = HD / 8;          // 16-byte chunks per K row
@@ -178,14 +179,16 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
   constexpr int RPI = 64 / KCH;        // K rows per DMA instruction
   constexpr int NKI = kKT / RPI / 4;   // K DMA instructions per wave per tile
   constexpr int NVI = HD / 8 / 4;      // V^T DMA instructions per wave per tile (8 rows each)
-  // two halves of 4 waves, each with a two-slot ring; every slot is its own variable
+  // H2 halves of 4 waves (the key range split in two inside the workgroup, or not),
+  // each with a two-slot ring; every slot is its own variable
+  constexpr int K2 = H2 == 2 ? K_BYTES : 16, V2 = H2 == 2 ? V_BYTES : 16;
   __shared__ __attribute__((aligned(16))) char ka0[K_BYTES], va0[V_BYTES], ka1[K_BYTES], va1[V_BYTES];
-  __shared__ __attribute__((aligned(16))) char kb0[K_BYTES], vb0[V_BYTES], kb1[K_BYTES], vb1[V_BYTES];
-  __shared__ __attribute__((aligned(16))) float comb[4 * 64 * 16];  // one O^T tile of the second half
-  __shared__ float cml[4 * 64 * 2];                                 // its running max and sum
+  __shared__ __attribute__((aligned(16))) char kb0[K2], vb0[V2], kb1[K2], vb1[V2];
+  __shared__ __attribute__((aligned(16))) float comb[H2 == 2 ? 4 * 64 * 16 : 4];  // one O^T tile of the second half
+  __shared__ float cml[H2 == 2 ? 4 * 64 * 2 : 2];                                 // its running max and sum
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int half = wave >> 2, qw = wave & 3;
+  const int half = H2 == 2 ? wave >> 2 : 0, qw = wave & 3;
   const int l32 = lane & 31, lg = lane >> 5;
 
   // workgroup -> (head group, query block, piece): heaviest blocks first, the pieces of
@@ -196,7 +199,7 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
   int wi = blockIdx.x / n_groups;
   int qblk = n_qblk - 1, npiece;
   for (;;) {
-    npiece = attn_pieces(attn_block_steps(qblk, PB, a.n, a.start_pos, a.capacity, (int)wlo), C);
+    npiece = attn_pieces(attn_block_steps(qblk, PB, a.n, a.start_pos, a.capacity, (int)wlo, H2), C);
     if (wi < npiece || qblk == 0) break;
     wi -= npiece;
     qblk--;
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
   const int tile0 = jlo / kKT, tile1 = jhi / kKT;                                 // inclusive
   // the first half takes the first ceil(n/2) tiles, the second half the rest; this
   // piece runs steps [sa, sb) of both
-  const int nsteps = (tile1 - tile0 + 2) / 2;
+  const int nsteps = (tile1 - tile0 + H2) / H2;
   const int sa = piece * nsteps / npiece, sb = (piece + 1) * nsteps / npiece;
   const int tb = (half ? tile0 + nsteps : tile0) + sa;
   const int te = min(half ? tile1 : tile0 + nsteps - 1, tb + (sb - sa) - 1);  // te < tb: nothing for this half
@@ -404,13 +407,15 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
       tile_work(k0, v0, tb + s);
     }
   };
-  if (half == 0) run(ka0, va0, ka1, va1);
+  if constexpr (H2 == 1) run(ka0, va0, ka1, va1);
+  else if (half == 0) run(ka0, va0, ka1, va1);
   else run(kb0, vb0, kb1, vb1);
   wait_vmcnt0();  // no DMA may still be writing this workgroup's LDS
   __syncthreads();
 
   // --- the second half hands its (m, l, O^T) to the first, one O^T tile at a time ---
   const int ci = (qw * 64 + lane);
+  if constexpr (H2 == 2) {
   if (half) {
     cml[2 * ci] = mrun;
     cml[2 * ci + 1] = lrun;
@@ -440,16 +445,20 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
     __syncthreads();
   }
   if (half) return;
+  }
 
   if (npiece > 1) {  // a piece of a split block: its partial (O^T, m, l) for the merge
-    constexpr int NF = part_fields<HD>();
-    float *rec = part + (((size_t)grp * n_qblk + qblk) * pmax + piece) * (size_t)(NF * 256) + ci;
+    constexpr int RF = part_rec_floats<HD>();
+    float *rec = part + (((size_t)grp * n_qblk + qblk) * pmax + piece) * (size_t)RF;
+    const float lt = lrun + __shfl_xor(lrun, 32, 64);  // the query's l (lane halves hold parts)
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    _Float16 *ro = reinterpret_cast<_Float16 *>(rec) + ci;
 #pragma unroll
     for (int i = 0; i < OT; i++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) rec[(16 * i + r) * 256] = o[i][r];
-    rec[(16 * OT) * 256] = mrun;
-    rec[(16 * OT + 1) * 256] = lrun;
+      for (int r = 0; r < 16; r++) ro[(16 * i + r) * 256] = (_Float16)(o[i][r] * inv);
+    rec[16 * OT * 128 + ci] = mrun;
+    rec[16 * OT * 128 + 256 + ci] = lt;
     return;
   }
 
@@ -475,12 +484,13 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(AttnArgs a, long wlo
 // same queries and O^T registers as in flash_attn_kernel.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, long wlo, int HG, int PB, int n_qblk,
-                                                         int n_hgrp, int C, const float *part, int pmax) {
+                                                         int n_hgrp, int C, const float *part, int pmax,
+                                                         int halves) {
   constexpr int OT = HD / 32;
-  constexpr int NF = part_fields<HD>();
+  constexpr int RF = part_rec_floats<HD>();
   constexpr int PMAX = 16;  // pieces combined per pass
   const int qblk = blockIdx.x, grp = blockIdx.y, i = blockIdx.z;  // i: the O^T tile (32 head-dim rows)
-  const int npiece = attn_pieces(attn_block_steps(qblk, PB, a.n, a.start_pos, a.capacity, (int)wlo), C);
+  const int npiece = attn_pieces(attn_block_steps(qblk, PB, a.n, a.start_pos, a.capacity, (int)wlo, halves), C);
   if (npiece < 2) return;  // written by flash_attn_kernel
   const int lane = threadIdx.x & 63, qw = threadIdx.x >> 6, ci = threadIdx.x;
   const int hgrp = grp % n_hgrp, kvh = grp / n_hgrp;
@@ -489,8 +499,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, long wlo, i
   const int h = kvh * G + hgrp * HG + hj;
   const int t = (qblk * PB + pb) * 32 + (lane & 31);
   const int lg = lane >> 5;
-  const float *rec0 = part + ((size_t)grp * n_qblk + qblk) * pmax * (size_t)(NF * 256) + ci;
-  // every load of a piece is issued before any is used
+  const float *rec0 = part + ((size_t)grp * n_qblk + qblk) * pmax * (size_t)RF;
+  // every load of a piece is issued before any is used; piece p contributes its
+  // normalized O with weight l_p * 2^(m_p - m)
   float m = -INFINITY, l = 0.0f, o[16];
 #pragma unroll
   for (int r = 0; r < 16; r++) o[r] = 0.0f;
@@ -498,7 +509,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, long wlo, i
     const int np = min(PMAX, npiece - p0);
     float mp[PMAX];
 #pragma unroll
-    for (int p = 0; p < PMAX; p++) mp[p] = p < np ? rec0[(size_t)(p0 + p) * NF * 256 + (16 * OT) * 256] : -INFINITY;
+    for (int p = 0; p < PMAX; p++) mp[p] = p < np ? rec0[(size_t)(p0 + p) * RF + 16 * OT * 128 + ci] : -INFINITY;
     float mm = m;
 #pragma unroll
     for (int p = 0; p < PMAX; p++) mm = fmaxf(mm, mp[p]);
@@ -509,18 +520,17 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, long wlo, i
     for (int r = 0; r < 16; r++) o[r] *= a0;
     m = mm;
     for (int p = 0; p < np; p++) {
-      const float *rec = rec0 + (size_t)(p0 + p) * NF * 256;
-      float v[17];
+      const float *rec = rec0 + (size_t)(p0 + p) * RF;
+      const _Float16 *ro = reinterpret_cast<const _Float16 *>(rec) + ci;
+      float v[16];
 #pragma unroll
-      for (int r = 0; r < 16; r++) v[r] = rec[(16 * i + r) * 256];
-      v[16] = rec[(16 * OT + 1) * 256];
-      const float sc = __builtin_amdgcn_exp2f(mp[p] - ms);
-      l += v[16] * sc;
+      for (int r = 0; r < 16; r++) v[r] = (float)ro[(16 * i + r) * 256];
+      const float w = rec[16 * OT * 128 + 256 + ci] * __builtin_amdgcn_exp2f(mp[p] - ms);
+      l += w;
 #pragma unroll
-      for (int r = 0; r < 16; r++) o[r] += v[r] * sc;
+      for (int r = 0; r < 16; r++) o[r] += v[r] * w;
     }
   }
-  l += __shfl_xor(l, 32, 64);
   if (t >= a.n) return;
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   _Float16 *dst = reinterpret_cast<_Float16 *>(a.out) + (size_t)t * a.n_head * HD + (size_t)h * HD;
@@ -535,12 +545,19 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, long wlo, i
 // Work split of one attention call.
 struct AttnPlan {
   int HG, PB, n_qblk, n_hgrp, C, pmax, pieces;  // pieces = workgroups per head group
+  int halves;                                   // key halves inside a workgroup (1 or 2)
 };
 
-AttnPlan plan_attention(const AttnArgs &a, const Window &w) {
+// Predicted time (us) of one layout, from workgroup costs measured on MI355X at
+// head_dim 128 (clock ramped; half the step cost at 64). Two key halves per
+// workgroup: one workgroup per CU, ~11.5 us fixed (Q load, first K/V tiles, merge of
+// the halves) + ~1.85 us per step of two tiles. One half: two workgroups per CU,
+// ~17 us fixed + ~0.9 us per tile. A split adds the merge kernel (~3 us plus its
+// partial traffic, written and read at cache rate).
+AttnPlan plan_layout(const AttnArgs &a, const Window &w, int halves, int force_c, double *t_out) {
   AttnPlan p;
-  // 4 query waves = HG heads of one KV group x PB blocks of 32 positions, twice (the
-  // two halves of the key range)
+  p.halves = halves;
+  // 4 query waves = HG heads of one KV group x PB blocks of 32 positions
   const int G = a.n_head / a.n_head_kv;
   p.HG = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
   p.PB = 4 / p.HG;
@@ -549,29 +566,31 @@ AttnPlan plan_attention(const AttnArgs &a, const Window &w) {
   const int n_groups = a.n_head_kv * p.n_hgrp;
   int maxs = 1;
   for (int b = 0; b < p.n_qblk; b++)
-    maxs = std::max(maxs, attn_block_steps(b, p.PB, a.n, a.start_pos, a.capacity, (int)w.lo));
-  // Piece size from the workgroup costs measured on MI355X at head_dim 128: about 8 us
-  // fixed (Q load, first K/V tiles, merge of the halves) plus 2 us per step, one
-  // workgroup per compute unit; a split adds the merge kernel (about 3 us plus its
-  // partial traffic). Half the step cost at head_dim 64.
-  const double cus = device_cu_count();
-  const double f = 8.0, g = a.head_dim > 64 ? 2.0 : 1.0;
-  const double rec_bytes = (16.0 * (a.head_dim / 32) + 2) * 256 * 4;
+    maxs = std::max(maxs, attn_block_steps(b, p.PB, a.n, a.start_pos, a.capacity, (int)w.lo, halves));
+  const double slots = (double)device_cu_count() * (halves == 2 ? 1 : 2);
+  const double hs = a.head_dim > 64 ? 1.0 : 0.5;
+  const double f = halves == 2 ? 11.5 : 17.0, g = (halves == 2 ? 1.85 : 0.9) * hs;
+  const double rec_bytes = (16.0 * (a.head_dim / 32) * 128 + 512) * 4;
   auto cost = [&](int C, int *pieces, int *pmax) {
     int np = 0, pm = 1, split_pieces = 0;
     for (int b = 0; b < p.n_qblk; b++) {
-      const int k = attn_pieces(attn_block_steps(b, p.PB, a.n, a.start_pos, a.capacity, (int)w.lo), C);
+      const int k = attn_pieces(attn_block_steps(b, p.PB, a.n, a.start_pos, a.capacity, (int)w.lo, halves), C);
       np += k;
       pm = std::max(pm, k);
       if (k > 1) split_pieces += k;
     }
     *pieces = np;
     *pmax = pm;
-    const double rounds = std::ceil((double)np * n_groups / cus);
+    const double rounds = std::ceil((double)np * n_groups / slots);
     double t = rounds * (f + g * std::min(C, maxs));
-    if (pm > 1) t += 3.0 + (double)split_pieces * n_groups * rec_bytes * 2 / 4e12 * 1e6;
+    if (pm > 1) t += 3.0 + (double)split_pieces * n_groups * rec_bytes * 2 / 10e12 * 1e6;
     return t;
   };
+  if (force_c > 0) {
+    p.C = std::min(force_c, maxs);
+    *t_out = cost(p.C, &p.pieces, &p.pmax);
+    return p;
+  }
   p.C = maxs;
   double best = cost(maxs, &p.pieces, &p.pmax);
   for (int C = 2; C < maxs; C++) {
@@ -584,7 +603,17 @@ AttnPlan plan_attention(const AttnArgs &a, const Window &w) {
       p.pmax = pm;
     }
   }
+  *t_out = best;
   return p;
+}
+
+// The cheaper of the two layouts (halves = 0), or the given one.
+AttnPlan plan_attention(const AttnArgs &a, const Window &w, int halves = 0, int force_c = 0) {
+  double t2, t1;
+  if (halves) return plan_layout(a, w, halves, force_c, &t2);
+  const AttnPlan p2 = plan_layout(a, w, 2, 0, &t2);
+  const AttnPlan p1 = plan_layout(a, w, 1, 0, &t1);
+  return t1 < t2 ? p1 : p2;
 }
 
 size_t window_bytes(const AttnArgs &a, const Window &w) {
@@ -593,8 +622,8 @@ size_t window_bytes(const AttnArgs &a, const Window &w) {
 
 size_t partial_bytes(const AttnArgs &a, const AttnPlan &p) {
   if (p.pmax < 2) return 0;
-  const size_t nf = 16 * (size_t)(a.head_dim / 32) + 2;
-  return (size_t)a.n_head_kv * p.n_hgrp * p.n_qblk * p.pmax * nf * 256 * 4;
+  const size_t rf = 16 * (size_t)(a.head_dim / 32) * 128 + 2 * 256;
+  return (size_t)a.n_head_kv * p.n_hgrp * p.n_qblk * p.pmax * rf * 4;
 }
 
 template <int HD>
@@ -607,13 +636,17 @@ int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
   const AttnPlan p = plan_attention(a, w);
   float *part = reinterpret_cast<float *>(reinterpret_cast<char *>(a.window) + window_bytes(a, w));
   const int n_groups = a.n_head_kv * p.n_hgrp;
-  hipLaunchKernelGGL((flash_attn_kernel<HD>), dim3(p.pieces * n_groups), dim3(512), 0, s, a, w.lo, w.pad, p.HG, p.PB,
-                     p.n_qblk, p.n_hgrp, p.C, part, p.pmax);
+  if (p.halves == 2)
+    hipLaunchKernelGGL((flash_attn_kernel<HD, 2>), dim3(p.pieces * n_groups), dim3(512), 0, s, a, w.lo, w.pad, p.HG,
+                       p.PB, p.n_qblk, p.n_hgrp, p.C, part, p.pmax);
+  else
+    hipLaunchKernelGGL((flash_attn_kernel<HD, 1>), dim3(p.pieces * n_groups), dim3(256), 0, s, a, w.lo, w.pad, p.HG,
+                       p.PB, p.n_qblk, p.n_hgrp, p.C, part, p.pmax);
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "flash_attn_kernel launch");
   if (p.pmax < 2) return SULIMO_HIP_OK;
   hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(p.n_qblk, n_groups, HD / 32), dim3(256), 0, s, a, w.lo, p.HG, p.PB,
-                     p.n_qblk, p.n_hgrp, p.C, part, p.pmax);
+                     p.n_qblk, p.n_hgrp, p.C, part, p.pmax, p.halves);
   e = hipGetLastError();
   return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "attn_merge_kernel launch");
 }
