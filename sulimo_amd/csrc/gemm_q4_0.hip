@@ -101,14 +101,48 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-template <int FM, int FN, int kNS, int EPI, int KSPLIT>
-__global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmArgs a) {
-  constexpr int BM = 32 * FM;
-  constexpr int BN = 128 * FN;                    // weight rows per tile (4 waves)
+// Lane exchanges within a quad of lanes (DPP quad_perm): partner lane j^1, j^2.
+__device__ __forceinline__ uint32_t dpp_xor1(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t dpp_xor2(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t fu(float v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ float uf(uint32_t v) { return __builtin_bit_cast(float, v); }
+
+// 4 x 4 transposes across a lane quad. Lane j of the quad holds rows 0..3 of column j;
+// afterwards it holds row j, columns 0..3. Every lane of the quad must be active.
+// f16: p = rows 0,1 and q = rows 2,3 (packed); returns columns 0,1 and 2,3 (packed).
+__device__ __forceinline__ uint2 quad_t16(uint32_t p, uint32_t q, int j) {
+  const uint32_t sel = (j & 1) ? 0x03020706u : 0x05040100u;
+  const uint32_t x = __builtin_amdgcn_perm(dpp_xor1(p), p, sel);  // row j&1 (odd) or 0, columns pair of j
+  const uint32_t y = __builtin_amdgcn_perm(dpp_xor1(q), q, sel);  // row 2 + (j&1)
+  const uint32_t r = dpp_xor2((j & 2) ? x : y);
+  return (j & 2) ? uint2{r, y} : uint2{x, r};
+}
+__device__ __forceinline__ float4 quad_t32(float a0, float a1, float a2, float a3, int j) {
+  const bool odd = j & 1, h = j & 2;
+  const float r1 = uf(dpp_xor1(fu(odd ? a0 : a1)));
+  const float r2 = uf(dpp_xor1(fu(odd ? a2 : a3)));
+  const float x0 = odd ? r1 : a0, x1 = odd ? a1 : r1;  // row j&1, the pair of columns holding j
+  const float y0 = odd ? r2 : a2, y1 = odd ? a3 : r2;  // row 2 + (j&1)
+  const float t0 = uf(dpp_xor2(fu(h ? x0 : y0))), t1 = uf(dpp_xor2(fu(h ? x1 : y1)));
+  return h ? float4{t0, t1, y0, y1} : float4{x0, x1, t0, t1};
+}
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+
+template <int FM, int FN, int kNS, int EPI, int KSPLIT, int WM>
+__global__ __launch_bounds__(256 * KSPLIT, WM == 2 ? 1 : 2 / KSPLIT) void gemm_q4_kernel(GemmArgs a) {
+  constexpr int WN = 4 / WM;                      // waves along the weight rows
+  constexpr int BM = 32 * FM * WM;
+  constexpr int BN = 32 * FN * WN;                // weight rows per tile
   constexpr bool kSwiglu = (EPI == EPI_SWIGLU);
   constexpr int OUT_BN = kSwiglu ? BN / 2 : BN;   // output columns per tile
-  constexpr int NX = FM;                          // X DMA instructions per wave per stage
-  constexpr int NQ = FN;                          // quant DMA instructions per wave per stage
+  constexpr int NX = FM * WM;                     // X DMA instructions per wave per stage
+  constexpr int NQ = FN * WN / 4;                 // quant DMA instructions per wave per stage
   constexpr int NDMA = NX + NQ + 1;               // + one scale DMA per wave per stage
   constexpr int X_BYTES = BM * kBK * 2;
   constexpr int Q_BYTES = BN * 32;
@@ -117,6 +151,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
   static_assert(!kSwiglu || FN % 2 == 0, "SwiGLU pairs gate and up fragments in one wave");
   static_assert(kNS >= 2 && kNS <= 6, "ring depth");
   static_assert(KSPLIT == 1 || KSPLIT == 2, "k split");
+  static_assert(WM == 1 || (WM == 2 && KSPLIT == 1 && FN % 2 == 0), "wave grid");
 
   // Ring slots of the (first) k half, and of the second when the workgroup splits K.
   __shared__ __attribute__((aligned(16))) char smem0[SLOT];
@@ -155,6 +190,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
   // wave = wave within its k half (4 per half); kh = the half of the K range it runs
   const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, kh = tid >> 8;
   const int l32 = lane & 31, lg = lane >> 5;
+  const int wave_m = wave % WM, wave_n = wave / WM;  // the wave's 32*FM rows and 32*FN weight rows
 
   // --- workgroup -> (K split, tile). Workgroups are dispatched round-robin over the
   // XCDs, each with its own L2: XCD e runs a contiguous range of the work order (split
@@ -189,44 +225,47 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
   const rsrc_t rx = make_rsrc(a.x, (uint32_t)a.m * (uint32_t)a.ldx * 2u);
   const rsrc_t rp = make_rsrc(seg.panels, (uint32_t)npanels * (uint32_t)nst * (uint32_t)kQ4PanelRecord);
 
-  // Wave w's fragment f -> panel (or -1 past the matrix). Fragment f covers output
-  // columns c0 + 32*(FN*w + f) ..; with SwiGLU the wave covers 16*FN columns, its
-  // first FN/2 fragments are their gate panels and the rest the up panels.
-  auto panel_of = [&](int f) -> int {
+  // Tile fragment g = FN*wn + f (fragment f of the waves at wave_n = wn) -> panel (or -1
+  // past the matrix). Fragment g covers output columns c0 + 32*g ..; with SwiGLU the
+  // waves at wn cover 16*FN columns, their first FN/2 fragments are the gate panels and
+  // the rest the up panels.
+  auto panel_of = [&](int g) -> int {
     int p;
     if constexpr (kSwiglu) {
-      const int j = c0 / 32 + wave * (FN / 2) + (f % (FN / 2));
+      const int wn = g / FN, f = g % FN;
+      const int j = c0 / 32 + wn * (FN / 2) + (f % (FN / 2));
       p = 2 * j + (f >= FN / 2 ? 1 : 0);
     } else {
-      p = c0 / 32 + FN * wave + f;
+      p = c0 / 32 + g;
     }
     return p < npanels ? p : -1;
   };
 
   // --- per-lane DMA offsets (bytes), fixed for the whole kernel ---
-  // X: wave instruction i covers tile rows 8*(FM*wave+i) .. +7; chunk c of row r lands at
+  // X: wave instruction i covers tile rows 8*(NX*wave+i) .. +7; chunk c of row r lands at
   // slot position c ^ ((r >> 1) & 7).
   uint32_t xoff[NX];
   bool xhi[NX];  // chunk in the stage's second block
 #pragma unroll
   for (int i = 0; i < NX; i++) {
-    const int row = 8 * (FM * wave + i) + (lane >> 3);
+    const int row = 8 * (NX * wave + i) + (lane >> 3);
     const int chunk = (lane & 7) ^ ((row >> 1) & 7);
     const int r = m0 + row;
     xoff[i] = r < a.m ? ((uint32_t)r * (uint32_t)a.ldx + 8u * chunk) * 2u : kOob;
     xhi[i] = chunk >= 4;
   }
-  // Quants: wave instruction f copies fragment f's 1 KB record run (lane = 16 bytes).
-  // Scales: lanes 8f .. 8f+7 of the wave's scale instruction copy fragment f's 128 bytes.
+  // Quants: wave instruction f copies tile fragment NQ*wave + f's 1 KB record run (lane =
+  // 16 bytes). Scales: lanes 8f .. 8f+7 of the wave's scale instruction copy tile
+  // fragment NQ*wave + f's 128 bytes.
   uint32_t qoff[NQ], soff;
 #pragma unroll
   for (int f = 0; f < NQ; f++) {
-    const int p = panel_of(f);
+    const int p = panel_of(NQ * wave + f);
     qoff[f] = p >= 0 ? (uint32_t)p * (uint32_t)nst * kQ4PanelRecord + 16u * lane : kOob;
   }
   {
-    const int f = lane >> 3;  // lanes past 8*FN never issue
-    const int p = f < FN ? panel_of(f) : -1;
+    const int f = lane >> 3;  // lanes past 8*NQ never issue
+    const int p = f < NQ ? panel_of(NQ * wave + f) : -1;
     soff = p >= 0 ? (uint32_t)p * (uint32_t)nst * kQ4PanelRecord + 1024u + 16u * (lane & 7) : kOob;
   }
 
@@ -240,11 +279,11 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
 #pragma unroll
     for (int i = 0; i < NX; i++) {
       const uint32_t off = (half && xhi[i]) ? kOob : xoff[i];
-      dma16(rx, slot + 8 * (FM * wave + i) * kBK * 2, off, sst * kBK * 2);
+      dma16(rx, slot + 8 * (NX * wave + i) * kBK * 2, off, sst * kBK * 2);
     }
 #pragma unroll
     for (int f = 0; f < NQ; f++) dma16(rp, slot + X_BYTES + (NQ * wave + f) * 1024, qoff[f], sst * kQ4PanelRecord);
-    if (lane < 8 * FN) dma16(rp, slot + X_BYTES + Q_BYTES + FN * wave * 128, soff, sst * kQ4PanelRecord);
+    if (lane < 8 * NQ) dma16(rp, slot + X_BYTES + Q_BYTES + NQ * wave * 128, soff, sst * kQ4PanelRecord);
   };
 
   floatx16 acc[FM][FN];
@@ -256,7 +295,7 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
   auto read_a = [&](const _Float16 *xb, int s, half8 (&ao)[FM]) {
 #pragma unroll
     for (int i = 0; i < FM; i++) {
-      const int row = 32 * i + l32;
+      const int row = 32 * (FM * wave_m + i) + l32;
       const int pos = (2 * s + lg) ^ ((row >> 1) & 7);
       ao[i] = *reinterpret_cast<const half8 *>(xb + row * kBK + 8 * pos);
     }
@@ -289,8 +328,8 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
     half2v d2[FN][2];
 #pragma unroll
     for (int f = 0; f < FN; f++) {
-      const int L = wave * 32 * FN + 32 * f + l32;
-      const uint4 qv = *reinterpret_cast<const uint4 *>(slot + X_BYTES + (FN * wave + f) * 1024 + 16 * lane);
+      const int L = wave_n * 32 * FN + 32 * f + l32;
+      const uint4 qv = *reinterpret_cast<const uint4 *>(slot + X_BYTES + (FN * wave_n + f) * 1024 + 16 * lane);
       q[f][0] = uint2{qv.x, qv.y};
       q[f][1] = uint2{qv.z, qv.w};
       const uint32_t w = *reinterpret_cast<const uint32_t *>(slot + X_BYTES + Q_BYTES + L * 4);
@@ -385,73 +424,97 @@ __global__ __launch_bounds__(256 * KSPLIT, 2 / KSPLIT) void gemm_q4_kernel(GemmA
     if (kh) return;
   }
 
-  // --- epilogue: acc register r of fragment (i, f) is C[8*(r/4) + 4*lg + r%4][l32] ---
+  // --- epilogue: acc register r of fragment (i, f) is C[8*(r/4) + 4*lg + r%4][l32]. Each
+  // group q of 4 registers (4 rows of one column) is transposed across the lane quad, so
+  // lane j of the quad stores row 8q + 4*lg + j, 4 consecutive columns, in one 8-byte
+  // (f16) or 16-byte (f32) store. Vector stores need 4-element aligned rows; the last
+  // group of a segment whose width is not a multiple of 4 stores element by element.
+  const int qj = lane & 3;
+  const int cq = 4 * (l32 >> 2);  // first column of the lane's 4 after the transpose
+  const bool vec_ok = ((seg.ldo | seg.col0) & 3) == 0 && ((uintptr_t)seg.out & 15) == 0;
 #pragma unroll
   for (int i = 0; i < FM; i++) {
-    if constexpr (kSwiglu) {
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
-        if (row >= a.m) continue;
+    for (int q = 0; q < 4; q++) {
+      const int row = m0 + 32 * (FM * wave_m + i) + 8 * q + 4 * lg + qj;
+      if constexpr (kSwiglu) {
 #pragma unroll
         for (int f = 0; f < FN / 2; f++) {
-          const int col = c0 + wave * 16 * FN + 32 * f + l32;
-          if (col >= seg.n) continue;
-          const float g = acc[i][f][r], u = acc[i][f + FN / 2][r];
-          const float silu = g / (1.0f + __expf(-g));
-          reinterpret_cast<_Float16 *>(seg.out)[(size_t)row * seg.ldo + seg.col0 + col] = (_Float16)(silu * u);
-        }
-      }
-    } else if constexpr (EPI == EPI_RESID) {
-      // x += f16(acc): all loads of the fragment row group first, then the stores
-      float old[16][FN];
+          float v[4];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
+          for (int e = 0; e < 4; e++) {
+            const float g = acc[i][f][4 * q + e], u = acc[i][f + FN / 2][4 * q + e];
+            v[e] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+          }
+          const uint2 o = quad_t16(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), qj);
+          const int col = c0 + wave_n * 16 * FN + 32 * f + cq;
+          if (row < a.m && col < seg.n) {
+            _Float16 *dst = reinterpret_cast<_Float16 *>(seg.out) + (size_t)row * seg.ldo + seg.col0 + col;
+            if (vec_ok && col + 4 <= seg.n) {
+              *reinterpret_cast<uint2 *>(dst) = o;
+            } else {
+              const uint32_t w[2] = {o.x, o.y};
+              for (int e = 0; e < 4 && col + e < seg.n; e++)
+                reinterpret_cast<uint16_t *>(dst)[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            }
+          }
+        }
+      } else {
 #pragma unroll
         for (int f = 0; f < FN; f++) {
-          const int col = c0 + wave * 32 * FN + 32 * f + l32;
-          old[r][f] = (row < a.m && col < seg.n)
-                          ? reinterpret_cast<const float *>(seg.out)[(size_t)row * seg.ldo + seg.col0 + col]
-                          : 0.0f;
-        }
-      }
+          const int lcol = c0 + wave_n * 32 * FN + 32 * f;  // first column of the fragment
+          float v[4];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
+          for (int e = 0; e < 4; e++) v[e] = acc[i][f][4 * q + e];
+          if constexpr (EPI == EPI_F16 || EPI == EPI_F32) {
+            if (seg.bias) {
+              const float b = lcol + l32 < seg.n ? seg.bias[lcol + l32] : 0.0f;
 #pragma unroll
-        for (int f = 0; f < FN; f++) {
-          const int col = c0 + wave * 32 * FN + 32 * f + l32;
-          if (row < a.m && col < seg.n)
-            reinterpret_cast<float *>(seg.out)[(size_t)row * seg.ldo + seg.col0 + col] =
-                old[r][f] + (float)(_Float16)acc[i][f][r];
-        }
-      }
-    } else if constexpr (EPI == EPI_PART) {
-      float *pb = a.part + (size_t)ks * a.m * a.ldp + colbase;
+              for (int e = 0; e < 4; e++) v[e] += b;
+            }
+          }
+          const int col = lcol + cq;
+          if constexpr (EPI == EPI_F16) {
+            const uint2 o = quad_t16(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), qj);
+            if (row < a.m && col < seg.n) {
+              _Float16 *dst = reinterpret_cast<_Float16 *>(seg.out) + (size_t)row * seg.ldo + seg.col0 + col;
+              if (vec_ok && col + 4 <= seg.n) {
+                *reinterpret_cast<uint2 *>(dst) = o;
+              } else {
+                const uint32_t w[2] = {o.x, o.y};
+                for (int e = 0; e < 4 && col + e < seg.n; e++)
+                  reinterpret_cast<uint16_t *>(dst)[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+              }
+            }
+          } else {
+            if constexpr (EPI == EPI_RESID) {
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
-        if (row >= a.m) continue;
-#pragma unroll
-        for (int f = 0; f < FN; f++) {
-          const int col = c0 + wave * 32 * FN + 32 * f + l32;
-          if (col < seg.n) pb[(size_t)row * a.ldp + col] = acc[i][f][r];
-        }
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
-        if (row >= a.m) continue;
-#pragma unroll
-        for (int f = 0; f < FN; f++) {
-          const int col = c0 + wave * 32 * FN + 32 * f + l32;
-          if (col >= seg.n) continue;
-          const size_t o = (size_t)row * seg.ldo + seg.col0 + col;
-          const float v = acc[i][f][r] + (seg.bias ? seg.bias[col] : 0.0f);
-          if constexpr (EPI == EPI_F16) reinterpret_cast<_Float16 *>(seg.out)[o] = (_Float16)v;
-          else reinterpret_cast<float *>(seg.out)[o] = v;
+              for (int e = 0; e < 4; e++) v[e] = (float)(_Float16)v[e];  // x += f16(acc)
+            }
+            const float4 o = quad_t32(v[0], v[1], v[2], v[3], qj);
+            if (row < a.m && col < seg.n) {
+              float *dst;
+              bool vec;
+              if constexpr (EPI == EPI_PART) {
+                dst = a.part + (size_t)ks * a.m * a.ldp + colbase + (size_t)row * a.ldp + col;
+                vec = col + 4 <= seg.n;  // partial planes are 4-column aligned
+              } else {
+                dst = reinterpret_cast<float *>(seg.out) + (size_t)row * seg.ldo + seg.col0 + col;
+                vec = vec_ok && col + 4 <= seg.n;
+              }
+              if (vec) {
+                float4 w = o;
+                if constexpr (EPI == EPI_RESID) {
+                  const float4 old = *reinterpret_cast<const float4 *>(dst);
+                  w = float4{old.x + o.x, old.y + o.y, old.z + o.z, old.w + o.w};
+                }
+                *reinterpret_cast<float4 *>(dst) = w;
+              } else {
+                const float w[4] = {o.x, o.y, o.z, o.w};
+                for (int e = 0; e < 4 && col + e < seg.n; e++) dst[e] = EPI == EPI_RESID ? dst[e] + w[e] : w[e];
+              }
+            }
+          }
         }
       }
     }
@@ -628,10 +691,10 @@ int normalize_splits(int k, int splits, int *split_stages) {
   return (nst + per - 1) / per;
 }
 
-template <int FM, int FN, int NS = 3, int KSPLIT = 1>
+template <int FM, int FN, int NS = 3, int KSPLIT = 1, int WM = 1>
 int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
-  constexpr int BM = 32 * FM;
-  constexpr int BN = 128 * FN;
+  constexpr int BM = 32 * FM * WM;
+  constexpr int BN = 32 * FN * (4 / WM);
   GemmArgs a = args;
   const int out_bn = (a.epi == EPI_SWIGLU) ? BN / 2 : BN;
   a.tiles_n = 0;
@@ -642,11 +705,11 @@ int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   a.splits = normalize_splits(a.k, a.splits, &a.split_stages);
   const dim3 grid(a.tiles_m * a.tiles_n * a.splits), block(256 * KSPLIT);
   switch (a.epi) {
-    case EPI_F16: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F16, KSPLIT>), grid, block, 0, s, a); break;
-    case EPI_F32: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F32, KSPLIT>), grid, block, 0, s, a); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_RESID, KSPLIT>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_SWIGLU, KSPLIT>), grid, block, 0, s, a); break;
-    case EPI_PART: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_PART, KSPLIT>), grid, block, 0, s, a); break;
+    case EPI_F16: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F16, KSPLIT, WM>), grid, block, 0, s, a); break;
+    case EPI_F32: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F32, KSPLIT, WM>), grid, block, 0, s, a); break;
+    case EPI_RESID: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_RESID, KSPLIT, WM>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_SWIGLU, KSPLIT, WM>), grid, block, 0, s, a); break;
+    case EPI_PART: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_PART, KSPLIT, WM>), grid, block, 0, s, a); break;
     default: return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "unknown GEMM epilogue");
   }
   const hipError_t e = hipGetLastError();
