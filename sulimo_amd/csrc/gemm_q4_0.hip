@@ -167,7 +167,6 @@ __global__ __launch_bounds__(256 * KSPLIT, WM == 2 ? 1 : 2 / KSPLIT) void gemm_q
   __shared__ __attribute__((aligned(16))) char smemb3[kNS > 3 ? SLOT2 : 16];
   __shared__ __attribute__((aligned(16))) char smemb4[kNS > 4 ? SLOT2 : 16];
   __shared__ __attribute__((aligned(16))) char smemb5[kNS > 5 ? SLOT2 : 16];
-  __shared__ __attribute__((aligned(16))) float comb[KSPLIT > 1 ? 256 * 16 : 4];  // one fragment of the second half
   auto slot_ptr = [&](auto H, auto J) -> char * {
     constexpr int j = decltype(J)::value % kNS;
     if constexpr (decltype(H)::value == 0) {
@@ -402,25 +401,28 @@ __global__ __launch_bounds__(256 * KSPLIT, WM == 2 ? 1 : 2 / KSPLIT) void gemm_q
   // no DMA may still be writing this workgroup's LDS when it exits
   wait_vmcnt<0>();
   if constexpr (KSPLIT > 1) {
-    // the second half hands its accumulators to the first, one fragment at a time
+    // The second half hands its accumulators to the first, 8 registers of a fragment at
+    // a time (8 KB), through a ring slot: every DMA has landed and every read is done.
+    static_assert(KSPLIT == 1 || SLOT >= 256 * 8 * 4, "combine buffer fits a ring slot");
+    float *cb = reinterpret_cast<float *>(smemb0) + (wave * 64 + lane) * 8;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-      for (int f = 0; f < FN; f++) {
-        float *cb = comb + (wave * 64 + lane) * 16;
-        if (kh) {
+      for (int f = 0; f < FN; f++)
 #pragma unroll
-          for (int r = 0; r < 16; r += 4)
-            *reinterpret_cast<float4 *>(cb + r) = float4{acc[i][f][r], acc[i][f][r + 1], acc[i][f][r + 2], acc[i][f][r + 3]};
-        }
-        __syncthreads();
-        if (!kh) {
+        for (int h = 0; h < 16; h += 8) {
+          if (kh) {
+            *reinterpret_cast<float4 *>(cb) = float4{acc[i][f][h], acc[i][f][h + 1], acc[i][f][h + 2], acc[i][f][h + 3]};
+            *reinterpret_cast<float4 *>(cb + 4) = float4{acc[i][f][h + 4], acc[i][f][h + 5], acc[i][f][h + 6], acc[i][f][h + 7]};
+          }
+          __syncthreads();
+          if (!kh) {
 #pragma unroll
-          for (int r = 0; r < 16; r++) acc[i][f][r] += cb[r];
+            for (int r = 0; r < 8; r++) acc[i][f][h + r] += cb[r];
+          }
+          __syncthreads();
         }
-        __syncthreads();
-      }
     if (kh) return;
   }
 
@@ -732,20 +734,23 @@ int device_cu_count() {
 namespace {
 
 // Tile configurations the planner chooses from (all with 3 ring slots).
-enum GemmCfg : int { kT32, kT32K2, kT64, kT64K2, kT128, kNumCfg };
-constexpr int kCfgRows[kNumCfg] = {32, 32, 64, 64, 128};
-constexpr int kCfgKsplit[kNumCfg] = {1, 2, 1, 2, 1};
+enum GemmCfg : int { kT32, kT32K2, kT64, kT64K2, kT128, kT128K2, kNumCfg };
+constexpr int kCfgRows[kNumCfg] = {32, 32, 64, 64, 128, 128};
+constexpr int kCfgKsplit[kNumCfg] = {1, 2, 1, 2, 1, 2};
 
-// Cost model fitted to measurements on MI355X (clock ramped) of the layer shapes at
-// M = 128 .. 3071 (median error 7 %): per workgroup, fixed + stages x per-stage (us),
-// the per-stage cost rising when two workgroups share a CU; a floor of the operand
-// bytes every workgroup pulls into LDS over the chip's fetch rate; a K split adds the
-// reduction kernel.
-constexpr double kCostFixed[kNumCfg] = {2.92, 3.77, 5.01, 6.34, 9.15};
-constexpr double kCostStage[kNumCfg] = {0.495, 0.744, 0.552, 0.939, 0.811};
-constexpr double kCostShared[kNumCfg] = {0.012, 0.0, 0.179, 0.0, 0.464};
-constexpr double kFetchMBperUs = 8.65;
-constexpr double kReduceFixed = 5.09, kReducePerMB = 0.144;
+// Cost model fitted to 1080 measurements on MI355X (clock ramped) of six layer shapes
+// (N x K = 2048 x 1536, 1536 x 1536, 8960 x 1536, 1536 x 8960, 256 x 1536, 3072 x 3072)
+// at M = 128 .. 3071, weighted to M = 512 and 2048 (median error 7 %; its picks sum to
+// within 1.5 % of the measured best): per workgroup,
+// fixed + stages x per-stage (us). The busiest CU runs ceil(workgroups / CUs) of them;
+// four-wave workgroups run in pairs, at a higher per-stage cost, and an odd last one
+// alone. The time is floored by the operand bytes every workgroup pulls into LDS over
+// the chip's fetch rate; a K split adds the reduction kernel.
+constexpr double kCostFixed[kNumCfg] = {2.36, 2.042, 3.977, 5.327, 6.75, 9.144};
+constexpr double kCostStage[kNumCfg] = {0.474, 0.704, 0.546, 0.939, 0.835, 1.503};
+constexpr double kCostShared[kNumCfg] = {0.147, 0.0, 0.353, 0.0, 0.682, 0.0};
+constexpr double kFetchMBperUs = 8.938;
+constexpr double kReduceFixed = 5.973, kReducePerMB = 0.1575;
 
 struct GemmPlan {
   int cfg;
@@ -766,10 +771,13 @@ double predict_us(const GemmArgs &a, int cfg, int splits, int cus) {
   for (int i = 0; i < a.nseg; i++) tn += (a.seg[i].n + out_bn - 1) / out_bn;
   const long wgs = (long)(a.m + kCfgRows[cfg] - 1) / kCfgRows[cfg] * tn * splits;
   const int stages = (per + kCfgKsplit[cfg] - 1) / kCfgKsplit[cfg];
-  const long load = (wgs + cus - 1) / cus;  // workgroups per CU
-  const int occ = kCfgKsplit[cfg] == 1 ? 2 : 1;
-  const long conc = std::min<long>(load, occ), seq = (load + occ - 1) / occ;
-  double t = seq * (kCostFixed[cfg] + stages * (kCostStage[cfg] + (conc - 1) * kCostShared[cfg]));
+  const long load = (wgs + cus - 1) / cus;  // workgroups on the busiest CU
+  const double alone = kCostFixed[cfg] + stages * kCostStage[cfg];
+  double t;
+  if (kCfgKsplit[cfg] == 1)  // two resident per CU
+    t = (load / 2) * (alone + stages * kCostShared[cfg]) + (load % 2) * alone;
+  else
+    t = load * alone;
   t = std::max(t, (double)wgs * per * (kCfgRows[cfg] * 128.0 + 9216.0) / 1e6 / kFetchMBperUs);
   if (splits > 1) {
     const double mn = (double)a.m * seg_cols(a);
@@ -815,7 +823,7 @@ GemmPlan plan_gemm(const GemmArgs &a, bool unbounded) {
       if (sp > 1 && t < tn) { tn = t; bestn = {cfg, sp}; }
     }
   }
-  return tn < 0.9 * t1 ? bestn : best1;  // split only for a clear predicted gain
+  return tn < t1 ? bestn : best1;
 }
 
 int32_t launch_plan(const GemmArgs &a, int cfg, hipStream_t s) {
@@ -824,7 +832,8 @@ int32_t launch_plan(const GemmArgs &a, int cfg, hipStream_t s) {
     case kT32K2: return launch_cfg<1, 2, 3, 2>(a, s);
     case kT64: return launch_cfg<2, 2, 3, 1>(a, s);
     case kT64K2: return launch_cfg<2, 2, 3, 2>(a, s);
-    default: return launch_cfg<4, 2, 3, 1>(a, s);
+    case kT128: return launch_cfg<4, 2, 3, 1>(a, s);
+    default: return launch_cfg<4, 2, 3, 2>(a, s);
   }
 }
 

@@ -72,17 +72,20 @@ def test_reference_patterns(ctx, n_tok, k, m_out):
     assert cosine(y, ref) >= 0.9999
 
 
-SHAPES = {  # (K, N) of the Qwen2.5-1.5B layer linears
+SHAPES = {  # (K, N) of the Qwen2.5-1.5B layer linears, and the Llama-3.2-3B QKV
     "q_o": (1536, 1536), "k_v": (1536, 256), "gate_up": (1536, 8960), "down": (8960, 1536),
+    "l3b_qkv": (3072, 5120),
 }
 
 
 @pytest.mark.parametrize("M,name", [(128, "gate_up"), (512, "q_o"), (512, "k_v"), (512, "gate_up"),
                                     (512, "down"), (37, "gate_up"), (1000, "q_o"), (3071, "k_v"),
-                                    (1, "down"), (8, "q_o")])
+                                    (1, "down"), (8, "q_o"), (1536, "down"), (1000, "l3b_qkv")])
 def test_benchmark_shapes_vs_fp32(ctx, M, name):
     """Benchmark shapes (nibbles uniform, d in [0.002, 0.02], x ~ N(0,1)) against an
-    fp32 reference: max rel err <= 1e-2 (denominator max(|ref|,1))."""
+    fp32 reference: max rel err <= 1e-2 (denominator max(|ref|,1)). Down at M = 1536
+    and the Llama QKV at M = 1000 run on 128 x 256 tiles with the K split inside the
+    workgroup (down also with K splits across workgroups)."""
     K, N = SHAPES[name]
     rng = np.random.default_rng(1000 + M + K + N)
     w = S.random_q4(rng, N, K)
