@@ -608,12 +608,35 @@ AttnPlan plan_layout(const AttnArgs &a, const Window &w, int halves, int force_c
 }
 
 // The cheaper of the two layouts (halves = 0), or the given one.
-AttnPlan plan_attention(const AttnArgs &a, const Window &w, int halves = 0, int force_c = 0) {
+AttnPlan plan_attention_uncached(const AttnArgs &a, const Window &w, int halves, int force_c) {
   double t2, t1;
   if (halves) return plan_layout(a, w, halves, force_c, &t2);
   const AttnPlan p2 = plan_layout(a, w, 2, 0, &t2);
   const AttnPlan p1 = plan_layout(a, w, 1, 0, &t1);
   return t1 < t2 ? p1 : p2;
+}
+
+// The plan depends only on the shape, the window (a function of the shape) and the CU
+// count; recent plans are kept per host thread (scoring every piece size over every
+// query block costs ~10 us, and every layer of a ubatch asks for the same plan).
+AttnPlan plan_attention(const AttnArgs &a, const Window &w, int halves = 0, int force_c = 0) {
+  struct Entry {
+    int key[9];
+    AttnPlan plan;
+  };
+  constexpr int kEntries = 8;
+  thread_local Entry cache[kEntries];
+  thread_local int used = 0, next = 0;
+  const int key[9] = {a.start_pos, a.n, a.capacity, a.n_head, a.n_head_kv, a.head_dim, halves, force_c,
+                      device_cu_count()};
+  for (int i = 0; i < used; i++)
+    if (std::equal(key, key + 9, cache[i].key)) return cache[i].plan;
+  const AttnPlan p = plan_attention_uncached(a, w, halves, force_c);
+  std::copy(key, key + 9, cache[next].key);
+  cache[next].plan = p;
+  next = (next + 1) % kEntries;
+  used = std::min(used + 1, kEntries);
+  return p;
 }
 
 size_t window_bytes(const AttnArgs &a, const Window &w) {

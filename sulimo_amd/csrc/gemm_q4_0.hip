@@ -797,7 +797,7 @@ bool can_split(const GemmArgs &a, int splits, bool unbounded) {
   return a.part && (size_t)splits * a.m * seg_cols(a) * 4 <= a.part_bytes;
 }
 
-GemmPlan plan_gemm(const GemmArgs &a, bool unbounded) {
+GemmPlan plan_gemm_uncached(const GemmArgs &a, bool unbounded) {
   const int cus = device_cu_count();
   if (a.epi == EPI_SWIGLU) {
     // measured rule: 128 x 256 tiles once they fill the GPU four times over
@@ -824,6 +824,34 @@ GemmPlan plan_gemm(const GemmArgs &a, bool unbounded) {
     }
   }
   return tn < t1 ? bestn : best1;
+}
+
+// Recent plans per host thread, keyed by everything the planner reads: the shape, the
+// epilogue, segment alignment (K splits need 4-column alignment), the partial workspace
+// and the CU count.
+GemmPlan plan_gemm(const GemmArgs &a, bool unbounded) {
+  constexpr int kKey = 16;
+  struct Entry {
+    long long key[kKey];
+    GemmPlan plan;
+  };
+  constexpr int kEntries = 16;
+  thread_local Entry cache[kEntries];
+  thread_local int used = 0, next = 0;
+  long long key[kKey] = {a.m, a.k, a.epi, a.nseg, unbounded, a.part != nullptr, (long long)a.part_bytes,
+                         device_cu_count()};
+  for (int i = 0; i < a.nseg; i++) {
+    key[8 + 2 * i] = a.seg[i].n;
+    key[9 + 2 * i] = (a.seg[i].ldo | a.seg[i].col0) & 3;
+  }
+  for (int i = 0; i < used; i++)
+    if (std::equal(key, key + kKey, cache[i].key)) return cache[i].plan;
+  const GemmPlan p = plan_gemm_uncached(a, unbounded);
+  std::copy(key, key + kKey, cache[next].key);
+  cache[next].plan = p;
+  next = (next + 1) % kEntries;
+  used = std::min(used + 1, kEntries);
+  return p;
 }
 
 int32_t launch_plan(const GemmArgs &a, int cfg, hipStream_t s) {
