@@ -162,7 +162,8 @@ __global__ __launch_bounds__(256) void kv_window_kernel(AttnArgs a, long wlo, in
 // 2. flash attention over the f16 window
 // ---------------------------------------------------------------------------
 // Split-key partial of one piece, per (query wave x lane) = 256 entries: the normalized
-// O^T registers O/l as f16 (16*OT fields of 256 f16), then m and the query's l as f32.
+// O^T registers O/l as f16, in 4*OT groups of 256 x 4 f16 (group 4i + g holds registers
+// 4g .. 4g+3 of O^T tile i, one 8-byte chunk per entry), then m and the query's l as f32.
 template <int HD>
 constexpr int part_rec_floats() { return 16 * (HD / 32) * 128 + 2 * 256; }
 
@@ -452,11 +453,13 @@ __global__ __launch_bounds__(256 * H2, 2 / H2) void flash_attn_kernel(AttnArgs a
     float *rec = part + (((size_t)grp * n_qblk + qblk) * pmax + piece) * (size_t)RF;
     const float lt = lrun + __shfl_xor(lrun, 32, 64);  // the query's l (lane halves hold parts)
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    _Float16 *ro = reinterpret_cast<_Float16 *>(rec) + ci;
+    half4 *ro = reinterpret_cast<half4 *>(rec) + ci;
 #pragma unroll
     for (int i = 0; i < OT; i++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) ro[(16 * i + r) * 256] = (_Float16)(o[i][r] * inv);
+      for (int g = 0; g < 4; g++)
+        ro[(4 * i + g) * 256] = half4{(_Float16)(o[i][4 * g] * inv), (_Float16)(o[i][4 * g + 1] * inv),
+                                      (_Float16)(o[i][4 * g + 2] * inv), (_Float16)(o[i][4 * g + 3] * inv)};
     rec[16 * OT * 128 + ci] = mrun;
     rec[16 * OT * 128 + 256 + ci] = lt;
     return;
@@ -521,10 +524,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, long wlo, i
     m = mm;
     for (int p = 0; p < np; p++) {
       const float *rec = rec0 + (size_t)(p0 + p) * RF;
-      const _Float16 *ro = reinterpret_cast<const _Float16 *>(rec) + ci;
+      const half4 *ro = reinterpret_cast<const half4 *>(rec) + ci;
       float v[16];
 #pragma unroll
-      for (int r = 0; r < 16; r++) v[r] = (float)ro[(16 * i + r) * 256];
+      for (int g = 0; g < 4; g++) {
+        const half4 hv = ro[(4 * i + g) * 256];
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[4 * g + e] = (float)hv[e];
+      }
       const float w = rec[16 * OT * 128 + 256 + ci] * __builtin_amdgcn_exp2f(mp[p] - ms);
       l += w;
 #pragma unroll
