@@ -17,6 +17,9 @@ per-launch GPU time taken from hipEvents recorded around every launch over K mor
 identical steps (the event records slow those steps, so they are kept out of
 `value`). `cpu_baseline` times the CPU oracle's restatement of the reference
 forward_token (AVX2, one pinned core) on a bounded sample of the same prompt.
+extra.llama3b_4x4096 is the prefill rate of a Llama-3.2-3B-shaped model (28 layers,
+hidden 3072, 24/8 heads, FFN 8192, vocab 128256) over 4 independent prompts of 4096
+tokens, each in one ubatch on a ring of 4096 positions.
 """
 from __future__ import annotations
 
@@ -50,6 +53,7 @@ def parse():
     ap.add_argument("--ubatch", type=int, default=2048)
     ap.add_argument("--cpu-sample", type=int, default=48, help="positions timed for the CPU baseline (0 = skip)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the per-shape GEMM table")
+    ap.add_argument("--no-llama", action="store_true", help="skip the Llama-3.2-3B 4 x 4096 prefill rate")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB three times (the known-size "
                          "reference for FETCH_SIZE/WRITE_SIZE counter passes) and exit")
@@ -117,6 +121,28 @@ def gemm_table(ctx, hip, S):
     out["layer_m512_total"] = {"us": round(tot_ms * 1e3, 2), "tflops": round(tot_flop / (tot_ms * 1e-3) / 1e12, 1),
                                "frac_mfma_peak": round(tot_flop / (tot_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4)}
     return out
+
+
+def llama_rate(ctx, hip, S, T=4096, prompts=4):
+    """Tokens/s of 4 independent 4096-token prefills (one ubatch each, ring of 4096) of a
+    random-init Llama-3.2-3B-shaped Q4_0 model, after one untimed pass over the prompts."""
+    cfg = S.LLAMA32_3B
+    hm = S.make_model(cfg, 0x5EED0003)
+    toks = [S.random_tokens(0x5EED1003 + i, T, cfg.vocab) for i in range(prompts)]
+    dm = hip.DeviceModel(ctx, hm, capacity=T, max_n=T)
+
+    def run():
+        for tk in toks:
+            dm.embed(tk)
+            dm.execute_prefill_ubatch(0, T)
+        ctx.wait()
+    run()
+    t0 = time.perf_counter()
+    run()
+    wall = time.perf_counter() - t0
+    dm.release()
+    return {"value": round(prompts * T / wall, 1), "unit": "tokens/s", "ms_per_prompt": round(wall / prompts * 1e3, 3),
+            "config": f"llama-3.2-3b-shaped q4_0, {prompts} prompts x {T} tokens, one ubatch each, ring {T}, last-token logits"}
 
 
 def cpu_baseline(hm, tokens, n_pos: int):
@@ -253,6 +279,8 @@ def main():
     if not a.no_gemm:
         extra["gemm_shapes"] = gemm_table(ctx, hip, S)
     dm.release()
+    if not a.no_llama:
+        extra["llama3b_4x4096"] = llama_rate(ctx, hip, S)
 
     cpu = None
     if a.cpu_sample > 0:
