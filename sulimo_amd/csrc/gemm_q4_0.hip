@@ -135,7 +135,7 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
 }
 
 template <int FM, int FN, int kNS, int EPI, int KSPLIT, int WM>
-__global__ __launch_bounds__(256 * KSPLIT, WM == 2 ? 1 : 2 / KSPLIT) void gemm_q4_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void gemm_q4_kernel(GemmArgs a) {
   constexpr int WN = 4 / WM;                      // waves along the weight rows
   constexpr int BM = 32 * FM * WM;
   constexpr int BN = 32 * FN * WN;                // weight rows per tile
@@ -150,43 +150,60 @@ __global__ __launch_bounds__(256 * KSPLIT, WM == 2 ? 1 : 2 / KSPLIT) void gemm_q
   constexpr int SLOT = X_BYTES + Q_BYTES + S_BYTES;
   static_assert(!kSwiglu || FN % 2 == 0, "SwiGLU pairs gate and up fragments in one wave");
   static_assert(kNS >= 2 && kNS <= 6, "ring depth");
-  static_assert(KSPLIT == 1 || KSPLIT == 2, "k split");
+  static_assert(KSPLIT == 1 || KSPLIT == 2 || (KSPLIT == 4 && FM == 1), "k split (four parts: 32-row tiles, 128 VGPRs a wave)");
   static_assert(WM == 1 || (WM == 2 && KSPLIT == 1 && FN % 2 == 0), "wave grid");
 
-  // Ring slots of the (first) k half, and of the second when the workgroup splits K.
+  // Ring slots of each part of the K range the workgroup splits (one part: no split).
+  constexpr int SLOT2 = KSPLIT > 1 ? SLOT : 16;
+  constexpr int SLOT4 = KSPLIT > 2 ? SLOT : 16;
   __shared__ __attribute__((aligned(16))) char smem0[SLOT];
   __shared__ __attribute__((aligned(16))) char smem1[SLOT];
   __shared__ __attribute__((aligned(16))) char smem2[kNS > 2 ? SLOT : 16];
   __shared__ __attribute__((aligned(16))) char smem3[kNS > 3 ? SLOT : 16];
   __shared__ __attribute__((aligned(16))) char smem4[kNS > 4 ? SLOT : 16];
   __shared__ __attribute__((aligned(16))) char smem5[kNS > 5 ? SLOT : 16];
-  constexpr int SLOT2 = KSPLIT > 1 ? SLOT : 16;
   __shared__ __attribute__((aligned(16))) char smemb0[SLOT2];
   __shared__ __attribute__((aligned(16))) char smemb1[SLOT2];
   __shared__ __attribute__((aligned(16))) char smemb2[kNS > 2 ? SLOT2 : 16];
   __shared__ __attribute__((aligned(16))) char smemb3[kNS > 3 ? SLOT2 : 16];
   __shared__ __attribute__((aligned(16))) char smemb4[kNS > 4 ? SLOT2 : 16];
   __shared__ __attribute__((aligned(16))) char smemb5[kNS > 5 ? SLOT2 : 16];
+  __shared__ __attribute__((aligned(16))) char smemc0[SLOT4];
+  __shared__ __attribute__((aligned(16))) char smemc1[SLOT4];
+  __shared__ __attribute__((aligned(16))) char smemc2[kNS > 2 ? SLOT4 : 16];
+  __shared__ __attribute__((aligned(16))) char smemd0[SLOT4];
+  __shared__ __attribute__((aligned(16))) char smemd1[SLOT4];
+  __shared__ __attribute__((aligned(16))) char smemd2[kNS > 2 ? SLOT4 : 16];
+  static_assert(KSPLIT < 4 || kNS == 3, "four K parts keep three ring slots each");
   auto slot_ptr = [&](auto H, auto J) -> char * {
     constexpr int j = decltype(J)::value % kNS;
-    if constexpr (decltype(H)::value == 0) {
+    constexpr int h = decltype(H)::value;
+    if constexpr (h == 0) {
       if constexpr (j == 0) return smem0;
       else if constexpr (j == 1) return smem1;
       else if constexpr (j == 2) return smem2;
       else if constexpr (j == 3) return smem3;
       else if constexpr (j == 4) return smem4;
       else return smem5;
-    } else {
+    } else if constexpr (h == 1) {
       if constexpr (j == 0) return smemb0;
       else if constexpr (j == 1) return smemb1;
       else if constexpr (j == 2) return smemb2;
       else if constexpr (j == 3) return smemb3;
       else if constexpr (j == 4) return smemb4;
       else return smemb5;
+    } else if constexpr (h == 2) {
+      if constexpr (j == 0) return smemc0;
+      else if constexpr (j == 1) return smemc1;
+      else return smemc2;
+    } else {
+      if constexpr (j == 0) return smemd0;
+      else if constexpr (j == 1) return smemd1;
+      else return smemd2;
     }
   };
 
-  // wave = wave within its k half (4 per half); kh = the half of the K range it runs
+  // wave = wave within its part of the K range (4 per part); kh = the part it runs
   const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, kh = tid >> 8;
   const int l32 = lane & 31, lg = lane >> 5;
   const int wave_m = wave % WM, wave_n = wave / WM;  // the wave's 32*FM rows and 32*FN weight rows
@@ -394,35 +411,43 @@ __global__ __launch_bounds__(256 * KSPLIT, WM == 2 ? 1 : 2 / KSPLIT) void gemm_q
   };
   if constexpr (KSPLIT == 1) {
     run(ic<0>{});
-  } else {
+  } else if constexpr (KSPLIT == 2) {
     if (kh == 0) run(ic<0>{});
     else run(ic<1>{});
+  } else {
+    if (kh == 0) run(ic<0>{});
+    else if (kh == 1) run(ic<1>{});
+    else if (kh == 2) run(ic<2>{});
+    else run(ic<3>{});
   }
   // no DMA may still be writing this workgroup's LDS when it exits
   wait_vmcnt<0>();
   if constexpr (KSPLIT > 1) {
-    // The second half hands its accumulators to the first, 8 registers of a fragment at
-    // a time (8 KB), through a ring slot: every DMA has landed and every read is done.
+    // Parts 1 .. KSPLIT-1 hand their accumulators to part 0 in turn, 8 registers of a
+    // fragment at a time (8 KB), through a ring slot: every DMA has landed and every
+    // read is done. Part 0 adds them in part order.
     static_assert(KSPLIT == 1 || SLOT >= 256 * 8 * 4, "combine buffer fits a ring slot");
     float *cb = reinterpret_cast<float *>(smemb0) + (wave * 64 + lane) * 8;
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+    for (int part = 1; part < KSPLIT; part++)
 #pragma unroll
-      for (int f = 0; f < FN; f++)
+      for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int h = 0; h < 16; h += 8) {
-          if (kh) {
-            *reinterpret_cast<float4 *>(cb) = float4{acc[i][f][h], acc[i][f][h + 1], acc[i][f][h + 2], acc[i][f][h + 3]};
-            *reinterpret_cast<float4 *>(cb + 4) = float4{acc[i][f][h + 4], acc[i][f][h + 5], acc[i][f][h + 6], acc[i][f][h + 7]};
+        for (int f = 0; f < FN; f++)
+#pragma unroll
+          for (int h = 0; h < 16; h += 8) {
+            if (kh == part) {
+              *reinterpret_cast<float4 *>(cb) = float4{acc[i][f][h], acc[i][f][h + 1], acc[i][f][h + 2], acc[i][f][h + 3]};
+              *reinterpret_cast<float4 *>(cb + 4) = float4{acc[i][f][h + 4], acc[i][f][h + 5], acc[i][f][h + 6], acc[i][f][h + 7]};
+            }
+            __syncthreads();
+            if (!kh) {
+#pragma unroll
+              for (int r = 0; r < 8; r++) acc[i][f][h + r] += cb[r];
+            }
+            __syncthreads();
           }
-          __syncthreads();
-          if (!kh) {
-#pragma unroll
-            for (int r = 0; r < 8; r++) acc[i][f][h + r] += cb[r];
-          }
-          __syncthreads();
-        }
     if (kh) return;
   }
 
@@ -710,7 +735,13 @@ int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
     case EPI_F16: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F16, KSPLIT, WM>), grid, block, 0, s, a); break;
     case EPI_F32: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F32, KSPLIT, WM>), grid, block, 0, s, a); break;
     case EPI_RESID: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_RESID, KSPLIT, WM>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_SWIGLU, KSPLIT, WM>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU:
+      if constexpr (FN % 2 == 0) {
+        hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_SWIGLU, KSPLIT, WM>), grid, block, 0, s, a);
+        break;
+      } else {
+        return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "SwiGLU tiles pair gate and up fragments (even FN)");
+      }
     case EPI_PART: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_PART, KSPLIT, WM>), grid, block, 0, s, a); break;
     default: return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "unknown GEMM epilogue");
   }
@@ -733,24 +764,28 @@ int device_cu_count() {
 
 namespace {
 
-// Tile configurations the planner chooses from (all with 3 ring slots).
-enum GemmCfg : int { kT32, kT32K2, kT64, kT64K2, kT128, kT128K2, kNumCfg };
-constexpr int kCfgRows[kNumCfg] = {32, 32, 64, 64, 128, 128};
-constexpr int kCfgKsplit[kNumCfg] = {1, 2, 1, 2, 1, 2};
+// Tile configurations the planner chooses from (all with 3 ring slots): token rows,
+// weight rows (128 * FN), K parts inside the workgroup, and the workgroups one CU holds
+// at once (registers and LDS of the compiled kernels).
+enum GemmCfg : int { kT32, kT32K2, kT64, kT64K2, kT128, kT128K2, kN32, kN32K2, kN32K4, kN64, kN64K2, kNumCfg };
+constexpr int kCfgRows[kNumCfg] = {32, 32, 64, 64, 128, 128, 32, 32, 32, 64, 64};
+constexpr int kCfgCols[kNumCfg] = {256, 256, 256, 256, 256, 256, 128, 128, 128, 128, 128};
+constexpr int kCfgKsplit[kNumCfg] = {1, 2, 1, 2, 1, 2, 1, 2, 4, 1, 2};
+constexpr int kCfgOcc[kNumCfg] = {4, 2, 3, 1, 2, 1, 6, 3, 1, 4, 2};
 
-// Cost model fitted to 1080 measurements on MI355X (clock ramped) of six layer shapes
+// Cost model fitted to 1980 measurements on MI355X (clock ramped) of six layer shapes
 // (N x K = 2048 x 1536, 1536 x 1536, 8960 x 1536, 1536 x 8960, 256 x 1536, 3072 x 3072)
-// at M = 128 .. 3071, weighted to M = 512 and 2048 (median error 7 %; its picks sum to
-// within 1.5 % of the measured best): per workgroup,
-// fixed + stages x per-stage (us). The busiest CU runs ceil(workgroups / CUs) of them;
-// four-wave workgroups run in pairs, at a higher per-stage cost, and an odd last one
-// alone. The time is floored by the operand bytes every workgroup pulls into LDS over
-// the chip's fetch rate; a K split adds the reduction kernel.
-constexpr double kCostFixed[kNumCfg] = {2.36, 2.042, 3.977, 5.327, 6.75, 9.144};
-constexpr double kCostStage[kNumCfg] = {0.474, 0.704, 0.546, 0.939, 0.835, 1.503};
-constexpr double kCostShared[kNumCfg] = {0.147, 0.0, 0.353, 0.0, 0.682, 0.0};
-constexpr double kFetchMBperUs = 8.938;
-constexpr double kReduceFixed = 5.973, kReducePerMB = 0.1575;
+// at M = 128 .. 3071 and S = 1 .. 8, weighted to M = 512 and 2048 (median error 6 %;
+// its picks sum to within 1.6 % of the measured best): per workgroup, fixed +
+// stages x per-stage (us). The busiest CU runs ceil(workgroups / CUs) of them in
+// rounds of up to kCfgOcc at once, the per-stage cost rising with each workgroup that
+// shares the CU. The time is floored by the operand bytes every workgroup pulls into
+// LDS over the chip's fetch rate; a K split adds the reduction kernel.
+constexpr double kCostFixed[kNumCfg] = {3.955, 4.070, 5.297, 5.459, 7.302, 9.483, 3.286, 3.221, 3.773, 4.174, 4.080};
+constexpr double kCostStage[kNumCfg] = {0.446, 0.754, 0.518, 0.952, 0.829, 1.507, 0.287, 0.454, 0.790, 0.321, 0.566};
+constexpr double kCostShared[kNumCfg] = {0.264, 0.474, 0.418, 0.0, 0.614, 0.0, 0.144, 0.289, 0.0, 0.212, 0.432};
+constexpr double kFetchMBperUs = 10.968;
+constexpr double kReduceFixed = 4.982, kReducePerMB = 0.1744;
 
 struct GemmPlan {
   int cfg;
@@ -766,19 +801,16 @@ int seg_cols(const GemmArgs &a) {
 double predict_us(const GemmArgs &a, int cfg, int splits, int cus) {
   int per;
   splits = normalize_splits(a.k, splits, &per);
-  const int out_bn = a.epi == EPI_SWIGLU ? 128 : 256;
+  const int out_bn = a.epi == EPI_SWIGLU ? kCfgCols[cfg] / 2 : kCfgCols[cfg];
   long tn = 0;
   for (int i = 0; i < a.nseg; i++) tn += (a.seg[i].n + out_bn - 1) / out_bn;
   const long wgs = (long)(a.m + kCfgRows[cfg] - 1) / kCfgRows[cfg] * tn * splits;
   const int stages = (per + kCfgKsplit[cfg] - 1) / kCfgKsplit[cfg];
   const long load = (wgs + cus - 1) / cus;  // workgroups on the busiest CU
-  const double alone = kCostFixed[cfg] + stages * kCostStage[cfg];
-  double t;
-  if (kCfgKsplit[cfg] == 1)  // two resident per CU
-    t = (load / 2) * (alone + stages * kCostShared[cfg]) + (load % 2) * alone;
-  else
-    t = load * alone;
-  t = std::max(t, (double)wgs * per * (kCfgRows[cfg] * 128.0 + 9216.0) / 1e6 / kFetchMBperUs);
+  const int occ = kCfgOcc[cfg];
+  auto round_us = [&](long c) { return kCostFixed[cfg] + stages * (kCostStage[cfg] + (c - 1) * kCostShared[cfg]); };
+  double t = (load / occ) * round_us(occ) + (load % occ ? round_us(load % occ) : 0.0);
+  t = std::max(t, (double)wgs * per * (kCfgRows[cfg] * 128.0 + kCfgCols[cfg] * 36.0) / 1e6 / kFetchMBperUs);
   if (splits > 1) {
     const double mn = (double)a.m * seg_cols(a);
     const double out_bytes = a.epi == EPI_RESID ? 8 : a.epi == EPI_F32 ? 4 : 2;
@@ -812,7 +844,7 @@ GemmPlan plan_gemm_uncached(const GemmArgs &a, bool unbounded) {
   double t1 = 1e30, tn = 1e30;
   static const int kSplits[] = {1, 2, 3, 4, 6, 8};
   for (int cfg = 0; cfg < kNumCfg; cfg++) {
-    if (kCfgKsplit[cfg] > 1 && a.k < 512) continue;  // at least two stages per half
+    if (kCfgKsplit[cfg] > 1 && a.k < 256 * kCfgKsplit[cfg]) continue;  // at least four stages per part
     if (kCfgRows[cfg] > 32 && a.m <= 32) continue;
     for (int sp : kSplits) {
       int per;
@@ -861,7 +893,12 @@ int32_t launch_plan(const GemmArgs &a, int cfg, hipStream_t s) {
     case kT64: return launch_cfg<2, 2, 3, 1>(a, s);
     case kT64K2: return launch_cfg<2, 2, 3, 2>(a, s);
     case kT128: return launch_cfg<4, 2, 3, 1>(a, s);
-    default: return launch_cfg<4, 2, 3, 2>(a, s);
+    case kT128K2: return launch_cfg<4, 2, 3, 2>(a, s);
+    case kN32: return launch_cfg<1, 1, 3, 1>(a, s);
+    case kN32K2: return launch_cfg<1, 1, 3, 2>(a, s);
+    case kN32K4: return launch_cfg<1, 1, 3, 4>(a, s);
+    case kN64: return launch_cfg<2, 1, 3, 1>(a, s);
+    default: return launch_cfg<2, 1, 3, 2>(a, s);
   }
 }
 
