@@ -273,14 +273,15 @@ __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
     int rope_dim, const float2 *cs_tab, int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
     int slot0, int wrap, const float *q_norm, const float *k_norm, float eps) {
   typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-  const int upw = head_dim / 8;  // units per head
+  // grid: x = token, y = blocks of 256 units (8 elements) of the token's q, k, v heads
+  const int upw = head_dim / 8;  // units per head (a power of two)
+  const int ush = __builtin_ctz(upw);
   const int slots = n_head + 2 * n_head_kv;
-  const long gid0 = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const bool valid = gid0 < (long)n * slots * upw;
-  const long gid = valid ? gid0 : 0;
-  const int u = (int)(gid % upw);
-  const long th = gid / upw;
-  const int hs = (int)(th % slots), t = (int)(th / slots);
+  const int t = blockIdx.x;
+  const int w0 = blockIdx.y * blockDim.x + threadIdx.x;
+  const bool valid = w0 < slots * upw;
+  const int w = valid ? w0 : 0;
+  const int u = w & (upw - 1), hs = w >> ush;
   const int half = rope_dim / 2;
   const int kvd = n_head_kv * head_dim;
   const int e0 = 8 * u;  // first element of the unit
@@ -294,9 +295,10 @@ __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
   half8 pv = xv;
   if (rot && mode != 0) pv = *reinterpret_cast<const half8 *>(src + (lo ? e0 + half : e0 - half));
   // q rotates in place and a NeoX partner unit belongs to another thread of the same
-  // workgroup (a head's units never straddle workgroups: 256 % (head_dim/8) == 0)
+  // workgroup (a head's units never straddle workgroups: 256 % (head_dim/8) == 0 and
+  // every workgroup starts at a head of one token)
   __syncthreads();
-  if (!valid) return;  // whole heads exit together (n * slots * head_dim/8 threads)
+  if (!valid) return;  // whole heads exit together (slots * head_dim/8 units a token)
   // optional QK-norm: RMSNorm of the head (its head_dim/8 consecutive lanes) with the
   // shared [head_dim] weights, before the rotation; partner values use the same scale
   float xf[8], pf[8];
@@ -367,7 +369,7 @@ __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
   const bool is_k = hs < n_head + n_head_kv;
   const int kvh = is_k ? hs - n_head : hs - n_head - n_head_kv;
   const size_t row_bytes = (size_t)n_head_kv * (head_dim / 32) * 34;
-  const int row = (int)(((long)slot0 + t) % wrap);
+  const int row = (slot0 + t) % wrap;  // slot0 + t fits int (positions are checked by the callers)
   uint8_t *blk = (is_k ? k_dst : v_dst) + (size_t)row * row_bytes + (size_t)kvh * (head_dim / 32) * 34 + (size_t)(u / 4) * 34;
   if ((u & 3) == 0) *reinterpret_cast<_Float16 *>(blk) = (_Float16)d;
   uint16_t *codes = reinterpret_cast<uint16_t *>(blk + 2 + 8 * (u & 3));  // 2-byte aligned
@@ -539,8 +541,8 @@ int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v,
   const size_t jobs = (size_t)n * (n_head + 2 * n_head_kv);
   if (jobs == 0) return SULIMO_HIP_OK;
   if (rope_dim % 16 == 0 && 256 % (head_dim / 8) == 0) {
-    const size_t units = jobs * (size_t)(head_dim / 8);
-    hipLaunchKernelGGL(rope_qkv_store_vec_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s,
+    const int units = (n_head + 2 * n_head_kv) * (head_dim / 8);  // per token
+    hipLaunchKernelGGL(rope_qkv_store_vec_kernel, dim3((unsigned)n, (unsigned)((units + 255) / 256)), dim3(256), 0, s,
                        reinterpret_cast<_Float16 *>(q), reinterpret_cast<const _Float16 *>(k),
                        reinterpret_cast<const _Float16 *>(v), n_head, n_head_kv, head_dim, rope_dim,
                        reinterpret_cast<const float2 *>(cs_tab), mode, n, k_dst, v_dst, slot0, wrap, q_norm,
