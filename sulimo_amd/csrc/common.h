@@ -124,12 +124,20 @@ struct GemmArgs {
   // Tile grid, filled by the launcher: tiles_m x tiles_n tiles, visited in groups of
   // group_m tile rows.
   int tiles_m, tiles_n, group_m;
+  // Optional RMSNorm of the rows an EPI_RESID GEMM updates (one segment of whole rows:
+  // col0 0, n the row width), run by the K-split reduction when the GEMM splits:
+  // norm_out[row] = f16(x * (1 / sqrt(mean(x^2) + norm_eps)) * norm_w) ([m][n]) and, if
+  // set, norm_x16[row] = f16(x). launch_gemm_q4_0 reports whether it ran it.
+  const float *norm_w;
+  uint16_t *norm_out, *norm_x16;
+  float norm_eps;
 };
 
 // Runs X W^T with the tile configuration and K split a cost model picks for the shape;
 // a K split writes f32 partials to a.part (a.part_bytes) and reduces them in a second
-// kernel.
-int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s);
+// kernel. With a.norm_w set and norm_done given, *norm_done tells whether that
+// reduction also produced the RMSNorm of the updated rows.
+int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done = nullptr);
 // Partial-sum workspace launch_gemm_q4_0 would use for this GEMM given unlimited room.
 size_t gemm_q4_0_workspace_bytes(const GemmArgs &a);
 

@@ -592,6 +592,70 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs a) {
   }
 }
 
+// K-split reduction of an EPI_RESID GEMM fused with the RMSNorm of the rows it updates:
+// one workgroup per row holding its V*1024 columns in registers. x += f16(partials summed
+// in split order (+ bias)), as split_reduce_kernel does, then norm_out = f16(x * scale *
+// norm_w) with scale = 1 / sqrt(mean(x^2) + eps), and norm_x16 = f16(x) when set.
+template <int V>
+__global__ __launch_bounds__(256) void split_reduce_norm_kernel(GemmArgs a) {
+  typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const GemmSegment seg = a.seg[0];
+  const int n4 = seg.n / 4;
+  const size_t plane = (size_t)a.m * a.ldp;
+  const float *p = a.part + (size_t)row * a.ldp;
+  float *x = reinterpret_cast<float *>(seg.out) + (size_t)row * seg.ldo;
+  float4 xv[V];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const int c4 = tid + 256 * j;
+    xv[j] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (c4 >= n4) continue;
+    float4 v = *reinterpret_cast<const float4 *>(p + 4 * c4);
+    for (int sp = 1; sp < a.splits; sp++) {
+      const float4 w = *reinterpret_cast<const float4 *>(p + sp * plane + 4 * c4);
+      v.x += w.x;
+      v.y += w.y;
+      v.z += w.z;
+      v.w += w.w;
+    }
+    if (seg.bias) {
+      const float4 b = *reinterpret_cast<const float4 *>(seg.bias + 4 * c4);
+      v.x += b.x;
+      v.y += b.y;
+      v.z += b.z;
+      v.w += b.w;
+    }
+    const float4 old = *reinterpret_cast<const float4 *>(x + 4 * c4);
+    const float4 nx = float4{old.x + (float)(_Float16)v.x, old.y + (float)(_Float16)v.y,
+                             old.z + (float)(_Float16)v.z, old.w + (float)(_Float16)v.w};
+    *reinterpret_cast<float4 *>(x + 4 * c4) = nx;
+    xv[j] = nx;
+    ss += nx.x * nx.x + nx.y * nx.y + nx.z * nx.z + nx.w * nx.w;
+  }
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) ss += __shfl_xor(ss, sh, 64);
+  __shared__ float red[4];
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  ss = red[0] + red[1] + red[2] + red[3];
+  const float scale = 1.0f / sqrtf(ss / (float)seg.n + a.norm_eps);
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const int c4 = tid + 256 * j;
+    if (c4 >= n4) continue;
+    const float4 w = *reinterpret_cast<const float4 *>(a.norm_w + 4 * c4);
+    const float4 nx = xv[j];
+    *reinterpret_cast<half4v *>(reinterpret_cast<_Float16 *>(a.norm_out) + (size_t)row * seg.n + 4 * c4) =
+        half4v{(_Float16)(nx.x * scale * w.x), (_Float16)(nx.y * scale * w.y), (_Float16)(nx.z * scale * w.z),
+               (_Float16)(nx.w * scale * w.w)};
+    if (a.norm_x16)
+      *reinterpret_cast<half4v *>(reinterpret_cast<_Float16 *>(a.norm_x16) + (size_t)row * seg.n + 4 * c4) =
+          half4v{(_Float16)nx.x, (_Float16)nx.y, (_Float16)nx.z, (_Float16)nx.w};
+  }
+}
+
 // GEMV for MT <= 4 tokens (decode, the last-token LM head): HBM-bound, so no MFMA and
 // no LDS staging of the weights. One wave per 32-row panel reads the panel's records
 // (lane l: quant bytes at 16*l, its row's two scales) U stages at a time, dequantizes
@@ -911,7 +975,8 @@ size_t gemm_q4_0_workspace_bytes(const GemmArgs &a) {
   return p.splits > 1 ? (size_t)p.splits * a.m * seg_cols(a) * 4 : 0;
 }
 
-int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
+int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done) {
+  if (norm_done) *norm_done = false;
   if (a.m <= 0) return SULIMO_HIP_OK;
   if (a.k <= 0 || a.k % 32 != 0) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM k must be a positive multiple of 32");
   if (a.ldx < a.k) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM activation row stride below k");
@@ -942,6 +1007,22 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s) {
   GemmArgs r = g;
   r.epi = a.epi;
   r.splits = normalize_splits(a.k, p.splits, &r.split_stages);
+  // the residual update and the RMSNorm of its rows in one pass, rows up to 8192 wide
+  const int v4 = (a.seg[0].n / 4 + 255) / 256;
+  if (norm_done && a.epi == EPI_RESID && a.norm_w && a.norm_out && a.nseg == 1 && a.seg[0].col0 == 0 && v4 <= 8) {
+    const dim3 grid((unsigned)a.m), block(256);
+    switch (v4) {
+      case 1: hipLaunchKernelGGL(split_reduce_norm_kernel<1>, grid, block, 0, s, r); break;
+      case 2: hipLaunchKernelGGL(split_reduce_norm_kernel<2>, grid, block, 0, s, r); break;
+      case 3: hipLaunchKernelGGL(split_reduce_norm_kernel<3>, grid, block, 0, s, r); break;
+      case 4: hipLaunchKernelGGL(split_reduce_norm_kernel<4>, grid, block, 0, s, r); break;
+      default: hipLaunchKernelGGL(split_reduce_norm_kernel<8>, grid, block, 0, s, r); break;
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "split_reduce_norm_kernel launch");
+    *norm_done = true;
+    return SULIMO_HIP_OK;
+  }
   const long threads = (long)a.m * (r.ldp / 4);
   const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
   switch (a.epi) {

@@ -504,15 +504,19 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
          return launch_rope_table(rope_tab, cfg->rope_dim, cfg->rope_base, (int)start_pos, in, s);
        })))
     return rc;
+  // An EPI_RESID GEMM whose K split runs the RMSNorm of the rows it updates (o-proj:
+  // the FFN norm, down-proj: the next layer's attention norm or the output norm) leaves
+  // h ready, and the separate norm launch is skipped.
+  bool h_ready = false;
   for (size_t l = 0; l < L; l++) {
     const sulimo_hip_layer_tensors &T = tensors->layers[l];
     uint8_t *ring_k = dp<uint8_t>(kv->k_buffers[l]);
     uint8_t *ring_v = dp<uint8_t>(kv->v_buffers[l]);
     // 1. attention RMSNorm
-    if ((rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
-           return launch_rmsnorm_f32(xres, dp<const float>(T.attn_norm), dp<uint16_t>(scratch->h), nullptr,
-                                     (int)D, cfg->eps, in, s);
-         })))
+    if (!h_ready && (rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
+                       return launch_rmsnorm_f32(xres, dp<const float>(T.attn_norm), dp<uint16_t>(scratch->h),
+                                                 nullptr, (int)D, cfg->eps, in, s);
+                     })))
       return rc;
     // panel copies of this layer's weights (built on the first ubatch)
     const uint8_t *pq, *pk, *pv, *po, *pgu, *pd;
@@ -588,12 +592,16 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     go.nseg = 1;
     go.part = gemm_part;
     go.part_bytes = gemm_ws;
-    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s); }))) return rc;
+    go.norm_w = dp<const float>(T.ffn_norm);
+    go.norm_out = dp<uint16_t>(scratch->h);
+    go.norm_eps = cfg->eps;
+    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s, &h_ready); })))
+      return rc;
     // 8. FFN RMSNorm
-    if ((rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
-           return launch_rmsnorm_f32(xres, dp<const float>(T.ffn_norm), dp<uint16_t>(scratch->h), nullptr,
-                                     (int)D, cfg->eps, in, s);
-         })))
+    if (!h_ready && (rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
+                       return launch_rmsnorm_f32(xres, dp<const float>(T.ffn_norm), dp<uint16_t>(scratch->h),
+                                                 nullptr, (int)D, cfg->eps, in, s);
+                     })))
       return rc;
     // 9-10. gate and up projections with SwiGLU fused into the epilogue
     GemmArgs gu{};
@@ -616,13 +624,19 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     gd.nseg = 1;
     gd.part = gemm_part;
     gd.part_bytes = gemm_ws;
-    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s); }))) return rc;
+    const bool last = l + 1 == L;
+    gd.norm_w = dp<const float>(last ? tensors->output_norm : tensors->layers[l + 1].attn_norm);
+    gd.norm_out = dp<uint16_t>(scratch->h);
+    gd.norm_x16 = last ? dp<uint16_t>(scratch->x) : nullptr;
+    gd.norm_eps = cfg->eps;
+    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s, &h_ready); })))
+      return rc;
   }
   // 13. output RMSNorm of all n rows (h), final residual back to scratch.x as f16
-  if ((rc = timed(ctx, PROF_NORM, 0, 8.0 * n * D + 4.0 * D, [&] {
-         return launch_rmsnorm_f32(xres, dp<const float>(tensors->output_norm), dp<uint16_t>(scratch->h),
-                                   dp<uint16_t>(scratch->x), (int)D, cfg->eps, in, s);
-       })))
+  if (!h_ready && (rc = timed(ctx, PROF_NORM, 0, 8.0 * n * D + 4.0 * D, [&] {
+                     return launch_rmsnorm_f32(xres, dp<const float>(tensors->output_norm), dp<uint16_t>(scratch->h),
+                                               dp<uint16_t>(scratch->x), (int)D, cfg->eps, in, s);
+                   })))
     return rc;
   // 14. logits of the last token
   const char *hlast = reinterpret_cast<const char *>(scratch->h->dev) + (n - 1) * D * 2;

@@ -136,6 +136,24 @@ def test_llama_3b_layer_shapes():
     dm.release()
 
 
+def test_split_down_projection_runs_the_next_norm():
+    """Two layers shaped so that the down projection (K = 4096) splits K across
+    workgroups: its reduction also writes the next layer's attention RMSNorm (layer 0)
+    and the output RMSNorm with the f16 residual (layer 1) in place of the separate norm
+    launches; matches the oracle in two chunks."""
+    cfg = S.ModelConfig(2, 1024, 4096, 8, 2, 128, 128, 512, 1e6, 1e-6, 1)
+    dm, okv, res = run_both(cfg, 77, [64, 40], 128)
+    for g, _, _, r in res:
+        assert np.max(np.abs(g - r)) <= 1e-2 * float(np.abs(r).max())
+        assert cosine(g, r) >= 0.999
+        assert int(np.argmax(g)) == int(np.argmax(r))
+    dk, dv = dm.kv_host()
+    for l in range(cfg.n_layers):
+        assert kv_within_one_step(dk[l], okv.k[l], np.arange(104), dm.bpp)
+        assert kv_within_one_step(dv[l], okv.v[l], np.arange(104), dm.bpp)
+    dm.release()
+
+
 def test_resume_at_1536_with_wrap_at_2048():
     """Edge-shape resume: 1536 positions written in ubatches of 512, then 1024 new tokens
     appended to the capacity-2048 ring, wrapping at 2048 (the last ubatch's queries see
