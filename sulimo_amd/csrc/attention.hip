@@ -105,18 +105,20 @@ Window window_of(const AttnArgs &a) {
 // ---------------------------------------------------------------------------
 // 1. Q8_0 window -> f16 K [kvh][pos][HD] and V^T [kvh][HD][pos]
 // ---------------------------------------------------------------------------
+// One wave per 16 window positions of one KV head (a 16-key group of the V^T chunk order).
+constexpr int kWinKeys = 16;
 template <int HD>
-__global__ __launch_bounds__(256) void kv_window_kernel(AttnArgs a, long wlo, int wlen, int wpad) {
+__global__ __launch_bounds__(64) void kv_window_kernel(AttnArgs a, long wlo, int wlen, int wpad) {
   constexpr int NB = HD / 32;
-  __shared__ _Float16 vt[kKT][HD + 2];
-  const int kvh = blockIdx.y, j0 = blockIdx.x * kKT;
+  __shared__ _Float16 vt[kWinKeys][HD + 2];
+  const int kvh = blockIdx.y, j0 = blockIdx.x * kWinKeys;
   const int cap = a.capacity;
   const size_t bpp = (size_t)a.n_head_kv * NB * 34;
   const size_t hoff = (size_t)kvh * NB * 34;
   _Float16 *kwin = reinterpret_cast<_Float16 *>(a.window);
   _Float16 *vwin = kwin + (size_t)a.n_head_kv * wpad * HD;
 
-  for (int job = threadIdx.x; job < kKT * NB; job += blockDim.x) {
+  for (int job = threadIdx.x; job < kWinKeys * NB; job += blockDim.x) {
     const int jj = job / NB, b = job % NB;
     const int j = j0 + jj;
     const long p = wlo + j;
@@ -149,8 +151,8 @@ __global__ __launch_bounds__(256) void kv_window_kernel(AttnArgs a, long wlo, in
   }
   __syncthreads();
   // V^T rows: chunk c (8 keys) of row h holds keys 16*(c/2) + kperm(8*(c%2) + e)
-  for (int job = threadIdx.x; job < HD * (kKT / 8); job += blockDim.x) {
-    const int h = job / (kKT / 8), c = job % (kKT / 8);
+  for (int job = threadIdx.x; job < HD * (kWinKeys / 8); job += blockDim.x) {
+    const int h = job / (kWinKeys / 8), c = job % (kWinKeys / 8);
     half8 v;
 #pragma unroll
     for (int e = 0; e < 8; e++) v[e] = vt[16 * (c >> 1) + kperm(8 * (c & 1) + e)][h];
@@ -659,7 +661,7 @@ size_t partial_bytes(const AttnArgs &a, const AttnPlan &p) {
 template <int HD>
 int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
   const Window w = window_of(a);
-  hipLaunchKernelGGL((kv_window_kernel<HD>), dim3(w.pad / kKT, a.n_head_kv), dim3(256), 0, s, a, w.lo, w.len,
+  hipLaunchKernelGGL((kv_window_kernel<HD>), dim3(w.pad / kWinKeys, a.n_head_kv), dim3(64), 0, s, a, w.lo, w.len,
                      w.pad);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "kv_window_kernel launch");
