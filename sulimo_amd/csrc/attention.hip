@@ -108,10 +108,10 @@ Window window_of(const AttnArgs &a) {
 // One wave per 16 window positions of one KV head (a 16-key group of the V^T chunk order).
 constexpr int kWinKeys = 16;
 template <int HD>
-__global__ __launch_bounds__(64) void kv_window_kernel(AttnArgs a, long wlo, int wlen, int wpad) {
+__global__ __launch_bounds__(64) void kv_window_kernel(AttnArgs a, long wlo, int wlen, int wpad, int jb0) {
   constexpr int NB = HD / 32;
   __shared__ _Float16 vt[kWinKeys][HD + 2];
-  const int kvh = blockIdx.y, j0 = blockIdx.x * kWinKeys;
+  const int kvh = blockIdx.y, j0 = (jb0 + (int)blockIdx.x) * kWinKeys;
   const int cap = a.capacity;
   const size_t bpp = (size_t)a.n_head_kv * NB * 34;
   const size_t hoff = (size_t)kvh * NB * 34;
@@ -661,10 +661,25 @@ size_t partial_bytes(const AttnArgs &a, const AttnPlan &p) {
 template <int HD>
 int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
   const Window w = window_of(a);
-  hipLaunchKernelGGL((kv_window_kernel<HD>), dim3(w.pad / kWinKeys, a.n_head_kv), dim3(64), 0, s, a, w.lo, w.len,
-                     w.pad);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "kv_window_kernel launch");
+  // window blocks of 16 positions: all of them, or (when the ubatch's own positions are
+  // already there) those holding earlier positions or padding; a block that also holds
+  // new positions rewrites them with the same values
+  auto window_blocks = [&](int b0, int b1) -> int32_t {
+    if (b1 <= b0) return SULIMO_HIP_OK;
+    hipLaunchKernelGGL((kv_window_kernel<HD>), dim3(b1 - b0, a.n_head_kv), dim3(64), 0, s, a, w.lo, w.len, w.pad, b0);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "kv_window_kernel launch");
+  };
+  const int nblk = w.pad / kWinKeys;
+  int32_t rc;
+  if (a.win_new_done) {
+    const int jn0 = (int)(a.start_pos - w.lo);  // window index of the first new position
+    const int pre = (jn0 + kWinKeys - 1) / kWinKeys, tail = w.len / kWinKeys;
+    if ((rc = window_blocks(0, pre)) || (rc = window_blocks(std::max(pre, tail), nblk))) return rc;
+  } else if ((rc = window_blocks(0, nblk))) {
+    return rc;
+  }
+  hipError_t e;
   const AttnPlan p = plan_attention(a, w);
   float *part = reinterpret_cast<float *>(reinterpret_cast<char *>(a.window) + window_bytes(a, w));
   const int n_groups = a.n_head_kv * p.n_hgrp;
@@ -684,6 +699,11 @@ int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
 }
 
 }  // namespace
+
+AttnWindowLayout attention_window_layout(const AttnArgs &a) {
+  const Window w = window_of(a);
+  return AttnWindowLayout{w.lo, w.len, w.pad, w.pad + kVPad};
+}
 
 size_t attention_workspace_bytes(const AttnArgs &a) {
   if (a.n <= 0 || a.n_head_kv <= 0 || a.n_head % a.n_head_kv != 0 || a.capacity <= 0) return 0;

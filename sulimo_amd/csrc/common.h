@@ -182,11 +182,19 @@ int32_t launch_embed_q4_0(const uint16_t *scales, const uint8_t *quants, const u
 int32_t launch_rope_table(float *tab, int rope_dim, float freq_base, int start_pos, int n, hipStream_t s);
 // q_norm / k_norm: optional f32 [head_dim] QK-norm weights (per-head RMSNorm with eps
 // before the rotation), or null.
+// Optional window target of the RoPE + Q8_0 store: the K rows and V^T columns of token
+// t go to window index j0 + t (the values f16(code * d) of the codes it stores).
+struct RopeWindowTarget {
+  uint16_t *k;  // f16 [n_head_kv][pad][head_dim]
+  uint16_t *vt; // f16 [n_head_kv][head_dim][vst]
+  int j0, pad, vst;
+};
 int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v, int n_head,
                               int n_head_kv, int head_dim, int rope_dim, const float *cs_tab,
                               int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
                               int slot0, int wrap, const float *q_norm, const float *k_norm,
-                              float eps, hipStream_t s);
+                              float eps, hipStream_t s, const RopeWindowTarget *win = nullptr,
+                              bool *wrote_window = nullptr);
 // Copies n rows of `row_bytes` from src to ring slots (slot0 + t) % capacity.
 int32_t launch_ring_commit(const uint8_t *src, uint8_t *ring, size_t row_bytes, int slot0,
                            int capacity, int n, hipStream_t s);
@@ -206,10 +214,29 @@ struct AttnArgs {
   // the visible key window, then the partial results of query blocks whose keys are
   // split over several workgroups.
   void *window;
+  // Nonzero when the caller already wrote the window entries of the ubatch's own
+  // positions [start_pos, start_pos + n) (the RoPE + Q8_0 store does, from the codes it
+  // stores); the window pass then covers only the earlier positions and the padding.
+  int win_new_done;
 };
 // Device bytes of AttnArgs::window for this attention call (depends on the shapes and
 // on the device's compute-unit count).
 size_t attention_workspace_bytes(const AttnArgs &a);
 int32_t launch_attention(const AttnArgs &a, hipStream_t s);
+
+// The f16 key window of an attention call: window index j holds position lo + j for
+// j < len (zeros up to pad); K is [n_head_kv][pad][head_dim] at AttnArgs::window, V^T
+// is [n_head_kv][head_dim][vst] after it.
+struct AttnWindowLayout {
+  long lo;
+  int len, pad, vst;
+};
+AttnWindowLayout attention_window_layout(const AttnArgs &a);
+// Column of window index j in a V^T row: inside each group of 16 keys, slots 4-7 and
+// 8-11 are swapped (the order in which the attention reads P^T operands).
+__host__ __device__ inline int window_vt_col(int j) {
+  const int s = j & 15;
+  return (j & ~15) + ((s & 4) ? ((s & 8) ? s : s + 4) : ((s & 8) ? s - 4 : s));
+}
 
 }  // namespace sulimo

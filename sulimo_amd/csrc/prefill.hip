@@ -542,17 +542,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     g.part = gemm_part;
     g.part_bytes = gemm_ws;
     if ((rc = timed(ctx, PROF_GEMM, gemm_flop(g), gemm_bytes(g), [&] { return launch_gemm_q4_0(g, s); }))) return rc;
-    // 3-4. RoPE on q and k, Q8_0 of k and v into the ring (or staging when wrapping)
-    if ((rc = timed(ctx, PROF_ROPE_KV, 0, 2.0 * n * (qd + 2 * kvd) + 2.0 * n * qd + 2.0 * n * bpp, [&] {
-           return launch_rope_qkv_store(dp<uint16_t>(scratch->q), dp<const uint16_t>(scratch->k),
-                                        dp<const uint16_t>(scratch->v), (int)Hq, (int)Hkv, (int)hd,
-                                        cfg->rope_dim, rope_tab, cfg->rope_mode, in,
-                                        staged ? stg_k : ring_k, staged ? stg_v : ring_v,
-                                        staged ? 0 : (int)(start_pos % cap), staged ? in : (int)cap,
-                                        opt_f32(T.attn_q_norm), opt_f32(T.attn_k_norm), cfg->eps, s);
-         })))
-      return rc;
-    // 5. causal GQA attention
+    // attention arguments first: the RoPE + Q8_0 store also writes the f16 window
+    // entries of the new positions
     AttnArgs at{};
     at.q = dp<const uint16_t>(scratch->q);
     at.out = dp<uint16_t>(scratch->attn_out);
@@ -568,6 +559,27 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     at.n_head_kv = (int)Hkv;
     at.head_dim = (int)hd;
     at.window = ws + off_w;
+    const AttnWindowLayout wl = attention_window_layout(at);
+    RopeWindowTarget wt{};
+    wt.k = reinterpret_cast<uint16_t *>(at.window);
+    wt.vt = wt.k + Hkv * (size_t)wl.pad * hd;
+    wt.j0 = (int)(start_pos - wl.lo);
+    wt.pad = wl.pad;
+    wt.vst = wl.vst;
+    bool wrote_window = false;
+    // 3-4. RoPE on q and k, Q8_0 of k and v into the ring (or staging when wrapping)
+    if ((rc = timed(ctx, PROF_ROPE_KV, 0, 2.0 * n * (qd + 2 * kvd) + 2.0 * n * qd + 2.0 * n * bpp, [&] {
+           return launch_rope_qkv_store(dp<uint16_t>(scratch->q), dp<const uint16_t>(scratch->k),
+                                        dp<const uint16_t>(scratch->v), (int)Hq, (int)Hkv, (int)hd,
+                                        cfg->rope_dim, rope_tab, cfg->rope_mode, in,
+                                        staged ? stg_k : ring_k, staged ? stg_v : ring_v,
+                                        staged ? 0 : (int)(start_pos % cap), staged ? in : (int)cap,
+                                        opt_f32(T.attn_q_norm), opt_f32(T.attn_k_norm), cfg->eps, s, &wt,
+                                        &wrote_window);
+         })))
+      return rc;
+    at.win_new_done = wrote_window ? 1 : 0;
+    // 5. causal GQA attention
     double keys = 0;  // sum over queries of visible keys
     for (size_t t = 0; t < n; t++) keys += (double)std::min(start_pos + t + 1, cap);
     const double kv_read = 2.0 * (double)std::min(start_pos + n, cap) * bpp;

@@ -271,7 +271,7 @@ __global__ __launch_bounds__(256) void rope_qkv_store_kernel(
 __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
     _Float16 *q, const _Float16 *k, const _Float16 *v, int n_head, int n_head_kv, int head_dim,
     int rope_dim, const float2 *cs_tab, int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
-    int slot0, int wrap, const float *q_norm, const float *k_norm, float eps) {
+    int slot0, int wrap, const float *q_norm, const float *k_norm, float eps, RopeWindowTarget win) {
   typedef _Float16 half8 __attribute__((ext_vector_type(8)));
   // grid: x = token, y = blocks of 256 units (8 elements) of the token's q, k, v heads
   const int upw = head_dim / 8;  // units per head (a power of two)
@@ -373,11 +373,26 @@ __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
   uint8_t *blk = (is_k ? k_dst : v_dst) + (size_t)row * row_bytes + (size_t)kvh * (head_dim / 32) * 34 + (size_t)(u / 4) * 34;
   if ((u & 3) == 0) *reinterpret_cast<_Float16 *>(blk) = (_Float16)d;
   uint16_t *codes = reinterpret_cast<uint16_t *>(blk + 2 + 8 * (u & 3));  // 2-byte aligned
+  float qc[8];
 #pragma unroll
   for (int j = 0; j < 8; j += 2) {
-    const float q0 = fminf(fmaxf(roundf(o[j] * id), -128.0f), 127.0f);
-    const float q1 = fminf(fmaxf(roundf(o[j + 1] * id), -128.0f), 127.0f);
-    codes[j / 2] = (uint16_t)((uint8_t)(int8_t)(int)q0 | ((uint16_t)(uint8_t)(int8_t)(int)q1 << 8));
+    qc[j] = fminf(fmaxf(roundf(o[j] * id), -128.0f), 127.0f);
+    qc[j + 1] = fminf(fmaxf(roundf(o[j + 1] * id), -128.0f), 127.0f);
+    codes[j / 2] = (uint16_t)((uint8_t)(int8_t)(int)qc[j] | ((uint16_t)(uint8_t)(int8_t)(int)qc[j + 1] << 8));
+  }
+  if (win.k) {  // the attention window entries of this position: f16(code * f16(d))
+    const float dq = (float)(_Float16)d;
+    const int j = win.j0 + t;
+    if (is_k) {
+      half8 r;
+#pragma unroll
+      for (int e = 0; e < 8; e++) r[e] = (_Float16)(qc[e] * dq);
+      *reinterpret_cast<half8 *>(reinterpret_cast<_Float16 *>(win.k) + ((size_t)kvh * win.pad + j) * head_dim + e0) = r;
+    } else {
+      _Float16 *vt = reinterpret_cast<_Float16 *>(win.vt) + ((size_t)kvh * head_dim + e0) * win.vst + window_vt_col(j);
+#pragma unroll
+      for (int e = 0; e < 8; e++) vt[(size_t)e * win.vst] = (_Float16)(qc[e] * dq);
+    }
   }
 }
 
@@ -535,7 +550,8 @@ int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v,
                               int n_head_kv, int head_dim, int rope_dim, const float *cs_tab,
                               int mode, int n, uint8_t *k_dst, uint8_t *v_dst,
                               int slot0, int wrap, const float *q_norm, const float *k_norm,
-                              float eps, hipStream_t s) {
+                              float eps, hipStream_t s, const RopeWindowTarget *win, bool *wrote_window) {
+  if (wrote_window) *wrote_window = false;
   if (head_dim > 256 || head_dim % 32 != 0)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "head_dim must be a multiple of 32 and <= 256");
   const size_t jobs = (size_t)n * (n_head + 2 * n_head_kv);
@@ -546,8 +562,10 @@ int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v,
                        reinterpret_cast<_Float16 *>(q), reinterpret_cast<const _Float16 *>(k),
                        reinterpret_cast<const _Float16 *>(v), n_head, n_head_kv, head_dim, rope_dim,
                        reinterpret_cast<const float2 *>(cs_tab), mode, n, k_dst, v_dst, slot0, wrap, q_norm,
-                       k_norm, eps);
-    return check_launch("rope_qkv_store_vec_kernel");
+                       k_norm, eps, win ? *win : RopeWindowTarget{});
+    const int32_t rc = check_launch("rope_qkv_store_vec_kernel");
+    if (rc == SULIMO_HIP_OK && win && wrote_window) *wrote_window = true;
+    return rc;
   }
   hipLaunchKernelGGL(rope_qkv_store_kernel, dim3(blocks_for(jobs, 4)), dim3(256), 0, s,
                      reinterpret_cast<_Float16 *>(q), reinterpret_cast<const _Float16 *>(k),
