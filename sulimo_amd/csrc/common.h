@@ -92,6 +92,7 @@ enum GemmEpilogue : int {
   EPI_RESID = 2,   // out f32 residual [rows][ldo] += f16(acc)
   EPI_SWIGLU = 3,  // out f16 [rows][ldo] = silu(acc_w0) * acc_w1 (w0 = gate, w1 = up)
   EPI_PART = 4,    // f32 partial sums of one K split: part[split][rows][ldp], reduced by a later kernel
+  EPI_ROPE = 5,    // q/k/v projection with RoPE and the Q8_0 K/V store (GemmArgs::rope)
 };
 
 // One weight matrix of a (possibly segmented) GEMM: `n` output rows, its
@@ -107,6 +108,27 @@ struct GemmSegment {
   const float *bias;  // optional f32 [n] added before the output rounding (F16/F32 epilogues)
 };
 
+// Optional window target of the RoPE + Q8_0 store: the K rows and V^T columns of token
+// t go to window index j0 + t (the values f16(code * d) of the codes it stores).
+struct RopeWindowTarget {
+  uint16_t *k;  // f16 [n_head_kv][pad][head_dim]
+  uint16_t *vt; // f16 [n_head_kv][head_dim][vst]
+  int j0, pad, vst;
+};
+// RoPE + Q8_0 K/V store of a q/k/v projection (EPI_ROPE). Segments 0, 1, 2 are q, k and
+// v of whole heads (rope_dim = head_dim, 64 or 128). q leaves rotated in f16 through
+// segment 0's output; k (rotated) and v are quantized to Q8_0 rows of row_bytes at
+// row (slot0 + t) % wrap of k_dst / v_dst, and with win.k set their window entries
+// f16(code * f16(d)) go to window index win.j0 + t. The values are those of
+// launch_rope_qkv_store applied to the f16 outputs of the plain projection.
+struct GemmRope {
+  const float *cs;  // float2 [m][head_dim / 2] cos/sin table of the ubatch
+  int mode;         // 0: pairs (2i, 2i+1), 1: NeoX pairs (i, i + head_dim/2)
+  int head_dim;
+  uint8_t *k_dst, *v_dst;
+  int slot0, wrap, row_bytes;
+  RopeWindowTarget win;
+};
 struct GemmArgs {
   const uint16_t *x;  // f16 [m][ldx]
   int m, k, ldx;
@@ -131,6 +153,7 @@ struct GemmArgs {
   const float *norm_w;
   uint16_t *norm_out, *norm_x16;
   float norm_eps;
+  GemmRope rope;  // EPI_ROPE only
 };
 
 // Runs X W^T with the tile configuration and K split a cost model picks for the shape;
@@ -182,13 +205,6 @@ int32_t launch_embed_q4_0(const uint16_t *scales, const uint8_t *quants, const u
 int32_t launch_rope_table(float *tab, int rope_dim, float freq_base, int start_pos, int n, hipStream_t s);
 // q_norm / k_norm: optional f32 [head_dim] QK-norm weights (per-head RMSNorm with eps
 // before the rotation), or null.
-// Optional window target of the RoPE + Q8_0 store: the K rows and V^T columns of token
-// t go to window index j0 + t (the values f16(code * d) of the codes it stores).
-struct RopeWindowTarget {
-  uint16_t *k;  // f16 [n_head_kv][pad][head_dim]
-  uint16_t *vt; // f16 [n_head_kv][head_dim][vst]
-  int j0, pad, vst;
-};
 int32_t launch_rope_qkv_store(uint16_t *q, const uint16_t *k, const uint16_t *v, int n_head,
                               int n_head_kv, int head_dim, int rope_dim, const float *cs_tab,
                               int mode, int n, uint8_t *k_dst, uint8_t *v_dst,

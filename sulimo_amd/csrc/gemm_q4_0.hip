@@ -448,7 +448,206 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
             }
             __syncthreads();
           }
-    if (kh) return;
+    // the RoPE epilogue's barriers need every wave
+    if constexpr (EPI != EPI_ROPE) {
+      if (kh) return;
+    }
+  }
+
+  if constexpr (EPI == EPI_ROPE) {
+    // --- RoPE + Q8_0 K/V store (segment 0: q, 1: k, 2: v; the tile holds whole heads).
+    // Per 32-row fragment i: the f16-rounded outputs (+ bias) are quad-transposed so that
+    // lane (qj, g = l32/4, lg) holds row 8q + 4lg + qj, columns 4g .. 4g+3 of fragment f.
+    // NeoX partners (column ^ head_dim/2) come through a [32][BN + 8] f16 exchange tile
+    // in ring slot 0. A Q8_0 block is one fragment's 32 columns of a row: 8 lanes (lane
+    // bits 2-4). The f16 window entries of v go to V^T rows after transposing back (lane
+    // = one column, 4 consecutive tokens). Every load of a fragment is issued before its
+    // first store (the stores could alias the table as far as the compiler knows), and
+    // the block maxima of all its rows reduce together.
+    const GemmRope &rp = a.rope;
+    const int hd = rp.head_dim, hsh = __builtin_ctz((unsigned)hd), hhalf = hd >> 1;
+    const bool neox = rp.mode != 0, rotate = si < 2;
+    constexpr int RS = BN + 8;  // exchange tile row stride (f16)
+    static_assert(32 * RS * 2 <= SLOT, "the exchange tile fits a ring slot");
+    _Float16 *xt = reinterpret_cast<_Float16 *>(smem0);
+    const int qj = lane & 3, cq = 4 * (l32 >> 2);
+    const bool work = kh == 0;  // K parts past the first only join the barriers
+    float bias[FN];  // of the lane's column before the transpose
+#pragma unroll
+    for (int f = 0; f < FN; f++) {
+      const int lcol = c0 + wave_n * 32 * FN + 32 * f;
+      bias[f] = (seg.bias && lcol + l32 < seg.n) ? seg.bias[lcol + l32] : 0.0f;
+    }
+    if constexpr (KSPLIT == 1) __syncthreads();  // every wave has finished reading the ring
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+      const int rbase = m0 + 32 * i + 4 * lg + qj;  // the lane's row for q = 0 (+ 8q)
+      uint2 xv[FN][4], pv[FN][4];
+#pragma unroll
+      for (int f = 0; f < FN; f++) {
+        const float b = bias[f];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          xv[f][q] = quad_t16(pack_h2(acc[i][f][4 * q] + b, acc[i][f][4 * q + 1] + b),
+                              pack_h2(acc[i][f][4 * q + 2] + b, acc[i][f][4 * q + 3] + b), qj);
+          pv[f][q] = xv[f][q];
+        }
+      }
+      // cos/sin of the lane's 4 elements (NeoX: 4 pairs from index e mod half; Norm: 2
+      // pairs from e/2), rows past the ubatch clamped to its last row
+      float4 ca[FN][4], cb[FN][4];
+      if (rotate && work) {
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+          const int e = (c0 + wave_n * 32 * FN + 32 * f + cq) & (hd - 1);
+          const int idx = neox ? (e < hhalf ? e : e - hhalf) : e / 2;
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int row = min(rbase + 8 * q, a.m - 1);
+            const float4 *cs = reinterpret_cast<const float4 *>(rp.cs + 2 * ((size_t)row * hhalf + idx));
+            ca[f][q] = cs[0];
+            cb[f][q] = neox ? cs[1] : ca[f][q];
+          }
+        }
+      }
+      if (rotate && neox) {
+        if (work) {
+#pragma unroll
+          for (int f = 0; f < FN; f++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+              *reinterpret_cast<uint2 *>(xt + (8 * q + 4 * lg + qj) * RS + wave_n * 32 * FN + 32 * f + cq) = xv[f][q];
+        }
+        __syncthreads();
+        if (work) {
+#pragma unroll
+          for (int f = 0; f < FN; f++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+              pv[f][q] = *reinterpret_cast<const uint2 *>(xt + (8 * q + 4 * lg + qj) * RS +
+                                                          ((wave_n * 32 * FN + 32 * f + cq) ^ hhalf));
+        }
+        __syncthreads();
+      }
+      if (!work) continue;
+      float o[FN][4][4];
+#pragma unroll
+      for (int f = 0; f < FN; f++) {
+        const int e = (c0 + wave_n * 32 * FN + 32 * f + cq) & (hd - 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const half2v x01 = as_h2(xv[f][q].x), x23 = as_h2(xv[f][q].y);
+          const float x[4] = {(float)x01[0], (float)x01[1], (float)x23[0], (float)x23[1]};
+#pragma unroll
+          for (int j = 0; j < 4; j++) o[f][q][j] = x[j];
+          if (!rotate) continue;
+          if (neox) {
+            const half2v p01 = as_h2(pv[f][q].x), p23 = as_h2(pv[f][q].y);
+            const float p[4] = {(float)p01[0], (float)p01[1], (float)p23[0], (float)p23[1]};
+            const float cc[4] = {ca[f][q].x, ca[f][q].z, cb[f][q].x, cb[f][q].z};
+            const float ss[4] = {ca[f][q].y, ca[f][q].w, cb[f][q].y, cb[f][q].w};
+            const bool lo = e < hhalf;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              if (lo) {
+                const float v0 = x[j], v1 = p[j];
+                o[f][q][j] = v0 * cc[j] - v1 * ss[j];
+              } else {
+                const float v0 = p[j], v1 = x[j];
+                o[f][q][j] = v0 * ss[j] + v1 * cc[j];
+              }
+            }
+          } else {
+            const float cc[2] = {ca[f][q].x, ca[f][q].z}, ss[2] = {ca[f][q].y, ca[f][q].w};
+#pragma unroll
+            for (int j = 0; j < 4; j += 2) {
+              const float v0 = x[j], v1 = x[j + 1];
+              o[f][q][j] = v0 * cc[j / 2] - v1 * ss[j / 2];
+              o[f][q][j + 1] = v0 * ss[j / 2] + v1 * cc[j / 2];
+            }
+          }
+        }
+      }
+      if (si == 0) {
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+          const int col = c0 + wave_n * 32 * FN + 32 * f + cq;  // the lane's first column in the segment
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const int row = rbase + 8 * q;
+            if (row < a.m && col < seg.n)
+              *reinterpret_cast<uint2 *>(reinterpret_cast<_Float16 *>(seg.out) + (size_t)row * seg.ldo + seg.col0 + col) =
+                  uint2{pack_h2(o[f][q][0], o[f][q][1]), pack_h2(o[f][q][2], o[f][q][3])};
+          }
+        }
+        continue;
+      }
+      // Q8_0 of each block (8 lanes, same row): amax, d = amax / 127, codes
+      float amax[FN][4];
+#pragma unroll
+      for (int f = 0; f < FN; f++)
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          amax[f][q] = fmaxf(fmaxf(fabsf(o[f][q][0]), fabsf(o[f][q][1])), fmaxf(fabsf(o[f][q][2]), fabsf(o[f][q][3])));
+#pragma unroll
+      for (int sh = 4; sh <= 16; sh *= 2)
+#pragma unroll
+        for (int f = 0; f < FN; f++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) amax[f][q] = fmaxf(amax[f][q], __shfl_xor(amax[f][q], sh, 64));
+      uint8_t *dst = si == 1 ? rp.k_dst : rp.v_dst;
+#pragma unroll
+      for (int f = 0; f < FN; f++) {
+        const int col = c0 + wave_n * 32 * FN + 32 * f + cq;
+        const int kvh = col >> hsh, e = col & (hd - 1);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int row = rbase + 8 * q;
+          const bool ok = row < a.m && col < seg.n;
+          const float d = amax[f][q] / 127.0f;
+          const float id = d != 0.0f ? 1.0f / d : 0.0f;
+          float qc[4];
+#pragma unroll
+          for (int j = 0; j < 4; j++) qc[j] = fminf(fmaxf(roundf(o[f][q][j] * id), -128.0f), 127.0f);
+          if (ok) {
+            int slot = rp.slot0 + row;
+            if (slot >= rp.wrap) slot %= rp.wrap;
+            uint8_t *blk = dst + (size_t)slot * rp.row_bytes + (size_t)(kvh * (hd >> 5) + (e >> 5)) * 34;
+            if ((e & 31) == 0) *reinterpret_cast<_Float16 *>(blk) = (_Float16)d;
+            uint16_t *codes = reinterpret_cast<uint16_t *>(blk + 2 + (e & 31));  // 2-byte aligned
+#pragma unroll
+            for (int j = 0; j < 4; j += 2)
+              codes[j / 2] = (uint16_t)((uint8_t)(int8_t)(int)qc[j] | ((uint16_t)(uint8_t)(int8_t)(int)qc[j + 1] << 8));
+          }
+          if (!rp.win.k) continue;
+          // window entries f16(code * f16(d))
+          const float dq = (float)(_Float16)d;
+          const uint2 w = uint2{pack_h2(qc[0] * dq, qc[1] * dq), pack_h2(qc[2] * dq, qc[3] * dq)};
+          if (si == 1) {
+            if (ok)
+              *reinterpret_cast<uint2 *>(reinterpret_cast<_Float16 *>(rp.win.k) +
+                                         ((size_t)kvh * rp.win.pad + rp.win.j0 + row) * hd + e) = w;
+          } else {
+            // back to one column per lane: column l32 of fragment f, tokens t0 .. t0+3
+            const uint2 wt = quad_t16(w.x, w.y, qj);
+            const int t0 = m0 + 32 * i + 8 * q + 4 * lg;
+            const int cv = c0 + wave_n * 32 * FN + 32 * f + l32;
+            if (t0 >= a.m || cv >= seg.n) continue;
+            _Float16 *vrow = reinterpret_cast<_Float16 *>(rp.win.vt) +
+                             ((size_t)(cv >> hsh) * hd + (cv & (hd - 1))) * rp.win.vst;
+            const int j = rp.win.j0 + t0;
+            if ((j & 3) == 0 && t0 + 3 < a.m) {
+              *reinterpret_cast<uint2 *>(vrow + window_vt_col(j)) = wt;  // 4 consecutive columns
+            } else {
+              const uint32_t ww[2] = {wt.x, wt.y};
+              for (int jj = 0; jj < 4 && t0 + jj < a.m; jj++)
+                reinterpret_cast<uint16_t *>(vrow)[window_vt_col(j + jj)] = (uint16_t)(ww[jj >> 1] >> (16 * (jj & 1)));
+            }
+          }
+        }
+      }
+    }
+    return;
   }
 
   // --- epilogue: acc register r of fragment (i, f) is C[8*(r/4) + 4*lg + r%4][l32]. Each
@@ -807,6 +1006,13 @@ int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
         return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "SwiGLU tiles pair gate and up fragments (even FN)");
       }
     case EPI_PART: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_PART, KSPLIT, WM>), grid, block, 0, s, a); break;
+    case EPI_ROPE:
+      if constexpr (WM == 1 && FN == 1) {
+        hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_ROPE, KSPLIT, WM>), grid, block, 0, s, a);
+        break;
+      } else {
+        return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "the RoPE epilogue runs on 128-column tiles");
+      }
     default: return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "unknown GEMM epilogue");
   }
   const hipError_t e = hipGetLastError();
@@ -893,6 +1099,10 @@ bool can_split(const GemmArgs &a, int splits, bool unbounded) {
   return a.part && (size_t)splits * a.m * seg_cols(a) * 4 <= a.part_bytes;
 }
 
+// The RoPE epilogue runs on 128-column tiles (one wave per 32 columns: its cos/sin,
+// partner and output registers fit beside the accumulators without spills).
+bool rope_tile_fits(int cfg) { return kCfgCols[cfg] == 128; }
+
 GemmPlan plan_gemm_uncached(const GemmArgs &a, bool unbounded) {
   const int cus = device_cu_count();
   if (a.epi == EPI_SWIGLU) {
@@ -910,6 +1120,7 @@ GemmPlan plan_gemm_uncached(const GemmArgs &a, bool unbounded) {
   for (int cfg = 0; cfg < kNumCfg; cfg++) {
     if (kCfgKsplit[cfg] > 1 && a.k < 256 * kCfgKsplit[cfg]) continue;  // at least four stages per part
     if (kCfgRows[cfg] > 32 && a.m <= 32) continue;
+    if (a.epi == EPI_ROPE && !rope_tile_fits(cfg)) continue;
     for (int sp : kSplits) {
       int per;
       if (normalize_splits(a.k, sp, &per) != sp) continue;
@@ -994,6 +1205,22 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done) {
   }
   if (a.epi == EPI_SWIGLU && a.nseg != 1)
     return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "SwiGLU GEMM takes one segment");
+  if (a.epi == EPI_ROPE) {
+    const GemmRope &r = a.rope;
+    const int hd = r.head_dim;
+    if (a.nseg != 3 || (hd != 64 && hd != 128))
+      return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "RoPE GEMM takes q, k, v segments of head_dim 64 or 128");
+    if (!r.cs || !r.k_dst || !r.v_dst || r.wrap <= 0 || r.slot0 < 0 || (r.mode != 0 && r.mode != 1))
+      return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "RoPE GEMM needs a cos/sin table, K/V targets and a ring size");
+    for (int i = 0; i < 3; i++)
+      if (a.seg[i].n % hd) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "RoPE GEMM segments must hold whole heads");
+    if (!a.seg[0].out || a.seg[0].ldo % 4 || a.seg[0].col0 % 4 || ((uintptr_t)a.seg[0].out & 7))
+      return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "RoPE GEMM q output must be 4-element aligned");
+    if (a.seg[1].n != a.seg[2].n || r.row_bytes != a.seg[1].n / 32 * 34)
+      return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "RoPE GEMM K/V rows must be the k and v widths in Q8_0");
+    if (r.win.k && (!r.win.vt || r.win.j0 < 0 || r.win.vst % 4 || ((uintptr_t)r.win.vt & 7) || ((uintptr_t)r.win.k & 7)))
+      return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "RoPE GEMM window target misaligned");
+  }
   if (gemv_fits(a)) return launch_gemv(a, s);
   const GemmPlan p = plan_gemm(a, false);
   if (p.splits == 1) return launch_plan(a, p.cfg, s);

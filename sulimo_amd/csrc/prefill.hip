@@ -528,20 +528,6 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
                             (int)D, &pgu)) ||
         (rc = get_q4_panels(ctx, T.ffn_down_scales, T.ffn_down_quants, nullptr, nullptr, (int)D, (int)F, &pd)))
       return rc;
-    // 2. q, k, v projections as one segmented GEMM
-    GemmArgs g{};
-    g.x = dp<const uint16_t>(scratch->h);
-    g.m = in;
-    g.k = (int)D;
-    g.ldx = (int)D;
-    g.epi = EPI_F16;
-    g.seg[0] = GemmSegment{pq, scratch->q->dev, (int)qd, (int)qd, 0, opt_f32(T.attn_q_bias)};
-    g.seg[1] = GemmSegment{pk, scratch->k->dev, (int)kvd, (int)kvd, 0, opt_f32(T.attn_k_bias)};
-    g.seg[2] = GemmSegment{pv, scratch->v->dev, (int)kvd, (int)kvd, 0, opt_f32(T.attn_v_bias)};
-    g.nseg = 3;
-    g.part = gemm_part;
-    g.part_bytes = gemm_ws;
-    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(g), gemm_bytes(g), [&] { return launch_gemm_q4_0(g, s); }))) return rc;
     // attention arguments first: the RoPE + Q8_0 store also writes the f16 window
     // entries of the new positions
     AttnArgs at{};
@@ -566,15 +552,34 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     wt.j0 = (int)(start_pos - wl.lo);
     wt.pad = wl.pad;
     wt.vst = wl.vst;
-    bool wrote_window = false;
+    uint8_t *k_dst = staged ? stg_k : ring_k, *v_dst = staged ? stg_v : ring_v;
+    const int slot0 = staged ? 0 : (int)(start_pos % cap), wrap = staged ? in : (int)cap;
+    // 2. q, k, v projections as one segmented GEMM. Without QK-norm and with a full-width
+    // rotation its epilogue also runs 3-4 (RoPE, Q8_0 of k and v, window entries); a
+    // ubatch of at most 4 tokens takes the GEMV and the separate kernel.
+    const bool fuse_rope = !opt_f32(T.attn_q_norm) && !opt_f32(T.attn_k_norm) && cfg->rope_dim == (int)hd &&
+                           (hd == 64 || hd == 128) && n > 4;
+    GemmArgs g{};
+    g.x = dp<const uint16_t>(scratch->h);
+    g.m = in;
+    g.k = (int)D;
+    g.ldx = (int)D;
+    g.epi = fuse_rope ? EPI_ROPE : EPI_F16;
+    g.seg[0] = GemmSegment{pq, scratch->q->dev, (int)qd, (int)qd, 0, opt_f32(T.attn_q_bias)};
+    g.seg[1] = GemmSegment{pk, scratch->k->dev, (int)kvd, (int)kvd, 0, opt_f32(T.attn_k_bias)};
+    g.seg[2] = GemmSegment{pv, scratch->v->dev, (int)kvd, (int)kvd, 0, opt_f32(T.attn_v_bias)};
+    g.nseg = 3;
+    g.part = gemm_part;
+    g.part_bytes = gemm_ws;
+    if (fuse_rope) g.rope = GemmRope{rope_tab, cfg->rope_mode, (int)hd, k_dst, v_dst, slot0, wrap, (int)bpp, wt};
+    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(g), gemm_bytes(g), [&] { return launch_gemm_q4_0(g, s); }))) return rc;
+    bool wrote_window = fuse_rope;
     // 3-4. RoPE on q and k, Q8_0 of k and v into the ring (or staging when wrapping)
-    if ((rc = timed(ctx, PROF_ROPE_KV, 0, 2.0 * n * (qd + 2 * kvd) + 2.0 * n * qd + 2.0 * n * bpp, [&] {
+    if (!fuse_rope && (rc = timed(ctx, PROF_ROPE_KV, 0, 2.0 * n * (qd + 2 * kvd) + 2.0 * n * qd + 2.0 * n * bpp, [&] {
            return launch_rope_qkv_store(dp<uint16_t>(scratch->q), dp<const uint16_t>(scratch->k),
                                         dp<const uint16_t>(scratch->v), (int)Hq, (int)Hkv, (int)hd,
-                                        cfg->rope_dim, rope_tab, cfg->rope_mode, in,
-                                        staged ? stg_k : ring_k, staged ? stg_v : ring_v,
-                                        staged ? 0 : (int)(start_pos % cap), staged ? in : (int)cap,
-                                        opt_f32(T.attn_q_norm), opt_f32(T.attn_k_norm), cfg->eps, s, &wt,
+                                        cfg->rope_dim, rope_tab, cfg->rope_mode, in, k_dst, v_dst, slot0,
+                                        wrap, opt_f32(T.attn_q_norm), opt_f32(T.attn_k_norm), cfg->eps, s, &wt,
                                         &wrote_window);
          })))
       return rc;

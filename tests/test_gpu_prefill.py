@@ -121,6 +121,25 @@ def test_resume_and_ring_wrap():
     dm.release()
 
 
+@pytest.mark.parametrize("cfg", [TINY_NEOX, TINY_NORM], ids=["neox", "norm"])
+def test_fused_rope_store_odd_ubatches(cfg):
+    """Ubatches of more than 4 tokens run RoPE, the Q8_0 K/V store and the attention-window
+    entries in the q/k/v GEMM's epilogue. Odd chunk sizes put the window start of the
+    second and fourth ubatch at positions 13 and 23 (element-wise V^T stores) and tiles
+    past the last token; the 3-token ubatch takes the GEMV and the separate kernel; the
+    last ubatch wraps the capacity-40 ring (staged K/V)."""
+    dm, okv, res = run_both(cfg, 41, [13, 7, 3, 21], 40)
+    for g, _, _, r in res:
+        assert np.max(np.abs(g - r)) <= 1e-2 * float(np.abs(r).max())
+        assert cosine(g, r) >= 0.999
+        assert int(np.argmax(g)) == int(np.argmax(r))
+    dk, dv = dm.kv_host()
+    for l in range(cfg.n_layers):
+        assert kv_within_one_step(dk[l], okv.k[l], np.arange(40), dm.bpp)
+        assert kv_within_one_step(dv[l], okv.v[l], np.arange(40), dm.bpp)
+    dm.release()
+
+
 def test_llama_3b_layer_shapes():
     """One layer of the Llama-3.2-3B shape (hidden 3072, FFN 8192, 24/8 heads, head_dim
     128, Norm RoPE base 5e5; small vocab for the oracle's sake), prefilled in two chunks."""
