@@ -422,6 +422,32 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   }
   // no DMA may still be writing this workgroup's LDS when it exits
   wait_vmcnt<0>();
+  // RoPE epilogue: cos/sin of the lane's 4 elements in fragment i (NeoX: 4 pairs from
+  // index e mod half; Norm: 2 pairs from e/2), rows past the ubatch clamped to its last
+  // row. Fragment 0's loads are issued here, under the K-part combine.
+  float4 rca[FN][4], rcb[FN][4];
+  auto rope_cs_load = [&](int i) __attribute__((always_inline)) {
+    if constexpr (EPI == EPI_ROPE) {
+      const int hd = a.rope.head_dim, hhalf = hd >> 1;
+      const bool neox = a.rope.mode != 0;
+      const int qj = lane & 3, cq = 4 * (l32 >> 2);
+#pragma unroll
+      for (int f = 0; f < FN; f++) {
+        const int e = (c0 + wave_n * 32 * FN + 32 * f + cq) & (hd - 1);
+        const int idx = neox ? (e < hhalf ? e : e - hhalf) : e / 2;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int row = min(m0 + 32 * i + 4 * lg + qj + 8 * q, a.m - 1);
+          const float4 *cs = reinterpret_cast<const float4 *>(a.rope.cs + 2 * ((size_t)row * hhalf + idx));
+          rca[f][q] = cs[0];
+          rcb[f][q] = neox ? cs[1] : rca[f][q];
+        }
+      }
+    }
+  };
+  if constexpr (EPI == EPI_ROPE) {
+    if (si < 2 && kh == 0) rope_cs_load(0);
+  }
   if constexpr (KSPLIT > 1) {
     // Parts 1 .. KSPLIT-1 hand their accumulators to part 0 in turn, 8 registers of a
     // fragment at a time (8 KB), through a ring slot: every DMA has landed and every
@@ -493,23 +519,8 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
           pv[f][q] = xv[f][q];
         }
       }
-      // cos/sin of the lane's 4 elements (NeoX: 4 pairs from index e mod half; Norm: 2
-      // pairs from e/2), rows past the ubatch clamped to its last row
-      float4 ca[FN][4], cb[FN][4];
-      if (rotate && work) {
-#pragma unroll
-        for (int f = 0; f < FN; f++) {
-          const int e = (c0 + wave_n * 32 * FN + 32 * f + cq) & (hd - 1);
-          const int idx = neox ? (e < hhalf ? e : e - hhalf) : e / 2;
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const int row = min(rbase + 8 * q, a.m - 1);
-            const float4 *cs = reinterpret_cast<const float4 *>(rp.cs + 2 * ((size_t)row * hhalf + idx));
-            ca[f][q] = cs[0];
-            cb[f][q] = neox ? cs[1] : ca[f][q];
-          }
-        }
-      }
+      if (i > 0 && rotate && work) rope_cs_load(i);  // fragment 0's were loaded before the combine
+      const auto &ca = rca, &cb = rcb;
       if (rotate && neox) {
         if (work) {
 #pragma unroll
@@ -1116,7 +1127,7 @@ GemmPlan plan_gemm_uncached(const GemmArgs &a, bool unbounded) {
   }
   GemmPlan best1{kT64, 1}, bestn{kT64, 1};
   double t1 = 1e30, tn = 1e30;
-  static const int kSplits[] = {1, 2, 3, 4, 6, 8};
+  static const int kSplits[] = {1, 2, 3, 4, 5, 6, 7, 8};
   for (int cfg = 0; cfg < kNumCfg; cfg++) {
     if (kCfgKsplit[cfg] > 1 && a.k < 256 * kCfgKsplit[cfg]) continue;  // at least four stages per part
     if (kCfgRows[cfg] > 32 && a.m <= 32) continue;
