@@ -85,13 +85,16 @@ def test_tiny_prefill_matches_oracle(cfg):
     dm.release()
 
 
-@pytest.mark.parametrize("cfg", [TINY_NEOX, TINY_NORM, S.ModelConfig(2, 256, 512, 4, 2, 64, 40, 512, 10000.0, 1e-6, 1)],
-                         ids=["neox", "norm", "neox_rope40"])
-def test_bias_and_qk_norm(cfg):
+@pytest.mark.parametrize("cfg,qk_norm", [(TINY_NEOX, True), (TINY_NORM, True),
+                                         (S.ModelConfig(2, 256, 512, 4, 2, 64, 40, 512, 10000.0, 1e-6, 1), True),
+                                         (TINY_NEOX, False), (TINY_NORM, False)],
+                         ids=["neox", "norm", "neox_rope40", "neox_bias_only", "norm_bias_only"])
+def test_bias_and_qk_norm(cfg, qk_norm):
     """Optional q/k/v biases and QK-norm (forward_pass.rs:250-272): added to the GEMM
     output before its f16 rounding, per-head RMSNorm before RoPE; matches the oracle
-    in two chunks and differs from the same model without them."""
-    dm, okv, res = run_both(cfg, 27, [16, 12], 64, biases=True, qk_norm=True)
+    in two chunks and differs from the same model without them. Biases without QK-norm
+    (Qwen2.5) run in the q/k/v GEMM's RoPE epilogue, the others in the separate kernel."""
+    dm, okv, res = run_both(cfg, 27, [16, 12], 64, biases=True, qk_norm=qk_norm)
     for g, _, _, r in res:
         scale = float(np.abs(r).max())
         assert np.max(np.abs(g - r)) <= 1e-2 * scale
