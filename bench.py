@@ -12,10 +12,12 @@ Prints one JSON line. Before the W warm-up steps, untimed steps run for at least
 half a second so that the GPU clock has left its idle state (counted under
 extra.prewarm). `value` is the rate of K timed steps with nothing else on the
 stream; extra.ubatch512 is the same prompt in the reference's default micro-batches
-of 512 tokens. `roofline` is the Q4_0 GEMM kernel (the dominant kernel), with its
-per-launch GPU time taken from hipEvents recorded around every launch over K more
-identical steps (the event records slow those steps, so they are kept out of
-`value`). `cpu_baseline` times the CPU oracle's restatement of the reference
+of 512 tokens, and extra.layer_m512_fused the per-layer time of their Q4_0 linears as
+the prefill runs them (QKV with the RoPE + KV-store epilogue, o, gate/up with SwiGLU,
+down with its residual + norm reduction). `roofline` is the Q4_0 GEMM kernel (the
+dominant kernel), with its per-launch GPU time taken from hipEvents recorded around
+every launch over K more identical steps (the event records slow those steps, so
+they are kept out of `value`). `cpu_baseline` times the CPU oracle's restatement of the reference
 forward_token (AVX2, one pinned core) on a bounded sample of the same prompt.
 extra.llama3b_4x4096 is the prefill rate of a Llama-3.2-3B-shaped model (28 layers,
 hidden 3072, 24/8 heads, FFN 8192, vocab 128256) over 4 independent prompts of 4096
@@ -276,6 +278,24 @@ def main():
         extra["ubatch512"] = {"value": round(T * a.steps / w512, 1), "unit": "tokens/s",
                               "ms_per_step": round(w512 / a.steps * 1e3, 3),
                               "config": f"the {T}-token prompt in {-(-T // 512)} micro-batches of 512"}
+        # The layer's linears at M=512 as the prefill runs them (QKV in one launch with the
+        # RoPE + KV-store epilogue, o with the residual, gate/up with SwiGLU, down split
+        # with its residual + RMSNorm reduction), per-launch events over the same steps.
+        ctx.set_profiling(True)
+        ctx.wait()
+        for _ in range(a.steps):
+            step512()
+        ctx.wait()
+        s5 = ctx.prefill_stats()
+        ctx.set_profiling(False)
+        n_layer_runs = a.steps * -(-T // 512) * cfg.n_layers
+        us = s5.gemm.total_ms * 1e3 / n_layer_runs
+        fl = 2.0 * 512 * cfg.embd * (cfg.q_dim + 2 * cfg.kv_dim + cfg.q_dim + 2 * cfg.ffn) + 2.0 * 512 * cfg.ffn * cfg.embd
+        extra["layer_m512_fused"] = {
+            "us": round(us, 2), "tflops": round(fl / (us * 1e-6) / 1e12, 1),
+            "frac_mfma_peak": round(fl / (us * 1e-6) / 1e12 / PEAK_F16_TFLOPS, 4),
+            "note": "GEMM-class time of the 512-token micro-batches per layer (includes the "
+                    "last-token LM head once per micro-batch, about 1 %)"}
     if not a.no_gemm:
         extra["gemm_shapes"] = gemm_table(ctx, hip, S)
     dm.release()

@@ -101,6 +101,14 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Workgroup barrier that orders LDS accesses only: global loads and stores in flight
+// stay in flight (__syncthreads also waits for those).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Lane exchanges within a quad of lanes (DPP quad_perm): partner lane j^1, j^2.
 __device__ __forceinline__ uint32_t dpp_xor1(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
@@ -422,10 +430,16 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   }
   // no DMA may still be writing this workgroup's LDS when it exits
   wait_vmcnt<0>();
+  // Accumulator register group q (registers 4q .. 4q+3: rows 8q + 4lg .. +3 of every
+  // fragment) belongs to K part q / NQO. After the combine each part holds the full sums
+  // of its NQO groups in registers 0 .. 4*NQO-1 and runs the epilogue for those rows:
+  // every wave of the workgroup shares the epilogue.
+  constexpr int NQO = 4 / KSPLIT;
+  const int qbase = kh * NQO;
   // RoPE epilogue: cos/sin of the lane's 4 elements in fragment i (NeoX: 4 pairs from
   // index e mod half; Norm: 2 pairs from e/2), rows past the ubatch clamped to its last
   // row. Fragment 0's loads are issued here, under the K-part combine.
-  float4 rca[FN][4], rcb[FN][4];
+  float4 rca[FN][NQO], rcb[FN][NQO];
   auto rope_cs_load = [&](int i) __attribute__((always_inline)) {
     if constexpr (EPI == EPI_ROPE) {
       const int hd = a.rope.head_dim, hhalf = hd >> 1;
@@ -436,47 +450,66 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
         const int e = (c0 + wave_n * 32 * FN + 32 * f + cq) & (hd - 1);
         const int idx = neox ? (e < hhalf ? e : e - hhalf) : e / 2;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const int row = min(m0 + 32 * i + 4 * lg + qj + 8 * q, a.m - 1);
+        for (int lq = 0; lq < NQO; lq++) {
+          const int row = min(m0 + 32 * i + 4 * lg + qj + 8 * (qbase + lq), a.m - 1);
           const float4 *cs = reinterpret_cast<const float4 *>(a.rope.cs + 2 * ((size_t)row * hhalf + idx));
-          rca[f][q] = cs[0];
-          rcb[f][q] = neox ? cs[1] : rca[f][q];
+          rca[f][lq] = cs[0];
+          rcb[f][lq] = cs[neox ? 1 : 0];  // unconditional load: no branch between the loads
         }
       }
     }
   };
-  if constexpr (EPI == EPI_ROPE) {
-    if (si < 2 && kh == 0) rope_cs_load(0);
-  }
+  // (loaded by every wave and tile, so that no branch joins the loads to their uses: the
+  // rows are clamped and the indices valid in every case)
+  if constexpr (EPI == EPI_ROPE) rope_cs_load(0);
   if constexpr (KSPLIT > 1) {
-    // Parts 1 .. KSPLIT-1 hand their accumulators to part 0 in turn, 8 registers of a
-    // fragment at a time (8 KB), through a ring slot: every DMA has landed and every
-    // read is done. Part 0 adds them in part order.
-    static_assert(KSPLIT == 1 || SLOT >= 256 * 8 * 4, "combine buffer fits a ring slot");
-    float *cb = reinterpret_cast<float *>(smemb0) + (wave * 64 + lane) * 8;
-    __syncthreads();
+    // Reduce-scatter through the parts' first ring slots (every DMA has landed and every
+    // ring read is done): in round o of a fragment the parts other than o write their
+    // registers 4*NQO*o .. +4*NQO-1, and part o adds all parts' values in part order,
+    // the sums the parts would give added into part 0 one after another.
+    constexpr int RG = 4 * NQO;  // registers per round
+    static_assert(SLOT >= 256 * RG * 4, "combine buffer fits a ring slot");
+    auto slot0 = [&](int part) -> float * {
+      return reinterpret_cast<float *>(part == 0 ? smem0 : part == 1 ? smemb0 : part == 2 ? smemc0 : smemd0);
+    };
+    const int cidx = (wave * 64 + lane) * RG;
+    float *mine = slot0(kh) + cidx;
+    lds_barrier();
 #pragma unroll
-    for (int part = 1; part < KSPLIT; part++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-      for (int i = 0; i < FM; i++)
+      for (int f = 0; f < FN; f++)
 #pragma unroll
-        for (int f = 0; f < FN; f++)
+        for (int o = 0; o < KSPLIT; o++) {
+          if (kh != o) {
 #pragma unroll
-          for (int h = 0; h < 16; h += 8) {
-            if (kh == part) {
-              *reinterpret_cast<float4 *>(cb) = float4{acc[i][f][h], acc[i][f][h + 1], acc[i][f][h + 2], acc[i][f][h + 3]};
-              *reinterpret_cast<float4 *>(cb + 4) = float4{acc[i][f][h + 4], acc[i][f][h + 5], acc[i][f][h + 6], acc[i][f][h + 7]};
-            }
-            __syncthreads();
-            if (!kh) {
-#pragma unroll
-              for (int r = 0; r < 8; r++) acc[i][f][h + r] += cb[r];
-            }
-            __syncthreads();
+            for (int r = 0; r < RG; r += 4)
+              *reinterpret_cast<float4 *>(mine + r) =
+                  float4{acc[i][f][RG * o + r], acc[i][f][RG * o + r + 1], acc[i][f][RG * o + r + 2], acc[i][f][RG * o + r + 3]};
           }
-    // the RoPE epilogue's barriers need every wave
-    if constexpr (EPI != EPI_ROPE) {
-      if (kh) return;
+          lds_barrier();
+          if (kh == o) {
+#pragma unroll
+            for (int r = 0; r < RG; r++) {
+              float v = o == 0 ? acc[i][f][RG * o + r] : slot0(0)[cidx + r];
+#pragma unroll
+              for (int p = 1; p < KSPLIT; p++) v += p == o ? acc[i][f][RG * o + r] : slot0(p)[cidx + r];
+              acc[i][f][RG * o + r] = v;
+            }
+          }
+          lds_barrier();
+        }
+    // the part's own groups to registers 0 .. RG-1 (static register indices)
+#pragma unroll
+    for (int o = 1; o < KSPLIT; o++) {
+      if (kh == o) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+          for (int f = 0; f < FN; f++)
+#pragma unroll
+            for (int r = 0; r < RG; r++) acc[i][f][r] = acc[i][f][RG * o + r];
+      }
     }
   }
 
@@ -489,7 +522,8 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     // bits 2-4). The f16 window entries of v go to V^T rows after transposing back (lane
     // = one column, 4 consecutive tokens). Every load of a fragment is issued before its
     // first store (the stores could alias the table as far as the compiler knows), and
-    // the block maxima of all its rows reduce together.
+    // the block maxima of all its rows reduce together. With K parts, each part does its
+    // own row groups.
     const GemmRope &rp = a.rope;
     const int hd = rp.head_dim, hsh = __builtin_ctz((unsigned)hd), hhalf = hd >> 1;
     const bool neox = rp.mode != 0, rotate = si < 2;
@@ -497,56 +531,50 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     static_assert(32 * RS * 2 <= SLOT, "the exchange tile fits a ring slot");
     _Float16 *xt = reinterpret_cast<_Float16 *>(smem0);
     const int qj = lane & 3, cq = 4 * (l32 >> 2);
-    const bool work = kh == 0;  // K parts past the first only join the barriers
     float bias[FN];  // of the lane's column before the transpose
 #pragma unroll
     for (int f = 0; f < FN; f++) {
       const int lcol = c0 + wave_n * 32 * FN + 32 * f;
       bias[f] = (seg.bias && lcol + l32 < seg.n) ? seg.bias[lcol + l32] : 0.0f;
     }
-    if constexpr (KSPLIT == 1) __syncthreads();  // every wave has finished reading the ring
+    if constexpr (KSPLIT == 1) lds_barrier();  // every wave has finished reading the ring
 #pragma unroll
     for (int i = 0; i < FM; i++) {
       const int rbase = m0 + 32 * i + 4 * lg + qj;  // the lane's row for q = 0 (+ 8q)
-      uint2 xv[FN][4], pv[FN][4];
+      uint2 xv[FN][NQO], pv[FN][NQO];
 #pragma unroll
       for (int f = 0; f < FN; f++) {
         const float b = bias[f];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          xv[f][q] = quad_t16(pack_h2(acc[i][f][4 * q] + b, acc[i][f][4 * q + 1] + b),
-                              pack_h2(acc[i][f][4 * q + 2] + b, acc[i][f][4 * q + 3] + b), qj);
-          pv[f][q] = xv[f][q];
+        for (int lq = 0; lq < NQO; lq++) {
+          xv[f][lq] = quad_t16(pack_h2(acc[i][f][4 * lq] + b, acc[i][f][4 * lq + 1] + b),
+                               pack_h2(acc[i][f][4 * lq + 2] + b, acc[i][f][4 * lq + 3] + b), qj);
+          pv[f][lq] = xv[f][lq];
         }
       }
-      if (i > 0 && rotate && work) rope_cs_load(i);  // fragment 0's were loaded before the combine
       const auto &ca = rca, &cb = rcb;
       if (rotate && neox) {
-        if (work) {
 #pragma unroll
-          for (int f = 0; f < FN; f++)
+        for (int f = 0; f < FN; f++)
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-              *reinterpret_cast<uint2 *>(xt + (8 * q + 4 * lg + qj) * RS + wave_n * 32 * FN + 32 * f + cq) = xv[f][q];
-        }
-        __syncthreads();
-        if (work) {
+          for (int lq = 0; lq < NQO; lq++)
+            *reinterpret_cast<uint2 *>(xt + (8 * (qbase + lq) + 4 * lg + qj) * RS + wave_n * 32 * FN + 32 * f + cq) =
+                xv[f][lq];
+        lds_barrier();
 #pragma unroll
-          for (int f = 0; f < FN; f++)
+        for (int f = 0; f < FN; f++)
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-              pv[f][q] = *reinterpret_cast<const uint2 *>(xt + (8 * q + 4 * lg + qj) * RS +
-                                                          ((wave_n * 32 * FN + 32 * f + cq) ^ hhalf));
-        }
-        __syncthreads();
+          for (int lq = 0; lq < NQO; lq++)
+            pv[f][lq] = *reinterpret_cast<const uint2 *>(xt + (8 * (qbase + lq) + 4 * lg + qj) * RS +
+                                                         ((wave_n * 32 * FN + 32 * f + cq) ^ hhalf));
+        lds_barrier();
       }
-      if (!work) continue;
-      float o[FN][4][4];
+      float o[FN][NQO][4];
 #pragma unroll
       for (int f = 0; f < FN; f++) {
         const int e = (c0 + wave_n * 32 * FN + 32 * f + cq) & (hd - 1);
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
+        for (int q = 0; q < NQO; q++) {  // q: the part's row group qbase + q
           const half2v x01 = as_h2(xv[f][q].x), x23 = as_h2(xv[f][q].y);
           const float x[4] = {(float)x01[0], (float)x01[1], (float)x23[0], (float)x23[1]};
 #pragma unroll
@@ -579,13 +607,16 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
           }
         }
       }
+      // the next fragment's cos/sin, issued before this fragment's stores (loads and
+      // stores retire in issue order, so its wait then covers no store)
+      if (i + 1 < FM) rope_cs_load(i + 1);
       if (si == 0) {
 #pragma unroll
         for (int f = 0; f < FN; f++) {
           const int col = c0 + wave_n * 32 * FN + 32 * f + cq;  // the lane's first column in the segment
 #pragma unroll
-          for (int q = 0; q < 4; q++) {
-            const int row = rbase + 8 * q;
+          for (int q = 0; q < NQO; q++) {
+            const int row = rbase + 8 * (qbase + q);
             if (row < a.m && col < seg.n)
               *reinterpret_cast<uint2 *>(reinterpret_cast<_Float16 *>(seg.out) + (size_t)row * seg.ldo + seg.col0 + col) =
                   uint2{pack_h2(o[f][q][0], o[f][q][1]), pack_h2(o[f][q][2], o[f][q][3])};
@@ -594,26 +625,26 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
         continue;
       }
       // Q8_0 of each block (8 lanes, same row): amax, d = amax / 127, codes
-      float amax[FN][4];
+      float amax[FN][NQO];
 #pragma unroll
       for (int f = 0; f < FN; f++)
 #pragma unroll
-        for (int q = 0; q < 4; q++)
+        for (int q = 0; q < NQO; q++)
           amax[f][q] = fmaxf(fmaxf(fabsf(o[f][q][0]), fabsf(o[f][q][1])), fmaxf(fabsf(o[f][q][2]), fabsf(o[f][q][3])));
 #pragma unroll
       for (int sh = 4; sh <= 16; sh *= 2)
 #pragma unroll
         for (int f = 0; f < FN; f++)
 #pragma unroll
-          for (int q = 0; q < 4; q++) amax[f][q] = fmaxf(amax[f][q], __shfl_xor(amax[f][q], sh, 64));
+          for (int q = 0; q < NQO; q++) amax[f][q] = fmaxf(amax[f][q], __shfl_xor(amax[f][q], sh, 64));
       uint8_t *dst = si == 1 ? rp.k_dst : rp.v_dst;
 #pragma unroll
       for (int f = 0; f < FN; f++) {
         const int col = c0 + wave_n * 32 * FN + 32 * f + cq;
         const int kvh = col >> hsh, e = col & (hd - 1);
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const int row = rbase + 8 * q;
+        for (int q = 0; q < NQO; q++) {
+          const int row = rbase + 8 * (qbase + q);
           const bool ok = row < a.m && col < seg.n;
           const float d = amax[f][q] / 127.0f;
           const float id = d != 0.0f ? 1.0f / d : 0.0f;
@@ -641,7 +672,7 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
           } else {
             // back to one column per lane: column l32 of fragment f, tokens t0 .. t0+3
             const uint2 wt = quad_t16(w.x, w.y, qj);
-            const int t0 = m0 + 32 * i + 8 * q + 4 * lg;
+            const int t0 = m0 + 32 * i + 8 * (qbase + q) + 4 * lg;
             const int cv = c0 + wave_n * 32 * FN + 32 * f + l32;
             if (t0 >= a.m || cv >= seg.n) continue;
             _Float16 *vrow = reinterpret_cast<_Float16 *>(rp.win.vt) +
@@ -661,7 +692,8 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     return;
   }
 
-  // --- epilogue: acc register r of fragment (i, f) is C[8*(r/4) + 4*lg + r%4][l32]. Each
+  // --- epilogue: acc register r of fragment (i, f) is C[8*(r/4) + 4*lg + r%4][l32], and
+  // after a K-part combine register 4*lq + e is row group q = qbase + lq. Each
   // group q of 4 registers (4 rows of one column) is transposed across the lane quad, so
   // lane j of the quad stores row 8q + 4*lg + j, 4 consecutive columns, in one 8-byte
   // (f16) or 16-byte (f32) store. Vector stores need 4-element aligned rows; the last
@@ -672,7 +704,8 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
 #pragma unroll
   for (int i = 0; i < FM; i++) {
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
+    for (int lq = 0; lq < NQO; lq++) {  // the part's row groups q = qbase + lq (registers 4*lq ..)
+      const int q = qbase + lq;
       const int row = m0 + 32 * (FM * wave_m + i) + 8 * q + 4 * lg + qj;
       if constexpr (kSwiglu) {
 #pragma unroll
@@ -680,7 +713,7 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            const float g = acc[i][f][4 * q + e], u = acc[i][f + FN / 2][4 * q + e];
+            const float g = acc[i][f][4 * lq + e], u = acc[i][f + FN / 2][4 * lq + e];
             v[e] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
           }
           const uint2 o = quad_t16(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), qj);
@@ -702,7 +735,7 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
           const int lcol = c0 + wave_n * 32 * FN + 32 * f;  // first column of the fragment
           float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; e++) v[e] = acc[i][f][4 * q + e];
+          for (int e = 0; e < 4; e++) v[e] = acc[i][f][4 * lq + e];
           if constexpr (EPI == EPI_F16 || EPI == EPI_F32) {
             if (seg.bias) {
               const float b = lcol + l32 < seg.n ? seg.bias[lcol + l32] : 0.0f;
