@@ -212,7 +212,10 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   };
 
   // wave = wave within its part of the K range (4 per part); kh = the part it runs
-  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3, kh = tid >> 8;
+  // wave and kh are wave-uniform: read into scalars, so that the LDS destinations of the
+  // DMA (M0) are computed once in scalar registers instead of per stage
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3), kh = __builtin_amdgcn_readfirstlane(tid >> 8);
   const int l32 = lane & 31, lg = lane >> 5;
   const int wave_m = wave % WM, wave_n = wave / WM;  // the wave's 32*FM rows and 32*FN weight rows
 
