@@ -716,7 +716,8 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            const float g = acc[i][f][4 * lq + e], u = acc[i][f + FN / 2][4 * lq + e];
+            // gate and up rounded to f16 first, as their separate GEMM outputs would be
+            const float g = (float)(_Float16)acc[i][f][4 * lq + e], u = (float)(_Float16)acc[i][f + FN / 2][4 * lq + e];
             v[e] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
           }
           const uint2 o = quad_t16(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), qj);
