@@ -154,6 +154,11 @@ struct GemmArgs {
   uint16_t *norm_out, *norm_x16;
   float norm_eps;
   GemmRope rope;  // EPI_ROPE only
+  // Persistent launch (filled by the launcher): fewer workgroups than tiles, each running
+  // a strided run of its XCD's tiles and loading the next tile's first stages under the
+  // current tile's epilogue. One segment, no split, an even block count, stages a
+  // multiple of the ring depth, and an epilogue that uses no LDS.
+  int persist;
 };
 
 // Runs X W^T with the tile configuration and K split a cost model picks for the shape;

@@ -224,16 +224,32 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   // major, then tiles), and the tile order walks group_m tile rows at a time, so the
   // workgroups resident on one XCD share their X rows and weight rows in its L2. Any
   // XCD count gives the same work items.
+  // Persistent mode (a.persist_wgs workgroups, one-part tiles of one segment, no split,
+  // an even block count and stages a multiple of NS): a workgroup runs every
+  // (workgroups per XCD)-th item of its XCD's range, and the last NS-1 refills of a tile
+  // load the next tile's first NS-1 stages into the same ring slots, so they land under
+  // the epilogue. Otherwise a workgroup runs one item.
   const int ntiles = a.tiles_m * a.tiles_n;
   const int nwork = ntiles * a.splits;
   const int xcd = blockIdx.x % kXcds, jx = blockIdx.x / kXcds;
-  const int w_item = xcd * (nwork / kXcds) + min(xcd, nwork % kXcds) + jx;
+  const int xlo = xcd * (nwork / kXcds) + min(xcd, nwork % kXcds);
+  const int xend = xlo + nwork / kXcds + (xcd < nwork % kXcds ? 1 : 0);
+  constexpr bool kCanPersist = KSPLIT == 1 && WM == 1 && (EPI == EPI_SWIGLU || EPI == EPI_F16 || EPI == EPI_F32 || EPI == EPI_RESID);
+  const int xstep = (kCanPersist && a.persist) ? (int)(gridDim.x / kXcds) : 0;
+  if (xlo + jx >= xend) return;  // persistent grid wider than the XCD's range
+  auto tile_of = [&](int w, int &tm, int &tn) {
+    const int tt = w % ntiles;
+    const int gr = tt / (a.group_m * a.tiles_n), tgg = tt - gr * a.group_m * a.tiles_n;
+    const int gmm = min(a.group_m, a.tiles_m - gr * a.group_m);
+    tm = gr * a.group_m + tgg % gmm;
+    tn = tgg / gmm;
+  };
+  bool primed = false;  // this tile's first NS-1 stages were issued by the previous tile
+  for (int w_item = xlo + jx;; w_item += xstep) {  // work items of this workgroup
+  const bool has_next = xstep > 0 && w_item + xstep < xend;
   const int ks = w_item / ntiles;
-  const int t = w_item - ks * ntiles;
-  const int grp = t / (a.group_m * a.tiles_n), tg = t - grp * a.group_m * a.tiles_n;
-  const int gm = min(a.group_m, a.tiles_m - grp * a.group_m);
-  const int tile_m = grp * a.group_m + tg % gm;
-  int tile_n = tg / gm;
+  int tile_m, tile_n;
+  tile_of(w_item, tile_m, tile_n);
   // --- tile -> (segment, first output column, first row) ---
   int si = 0, colbase = 0;  // colbase: columns of the segments before (partial sums)
   for (; si < a.nseg - 1; si++) {
@@ -295,12 +311,9 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     const int p = f < NQ ? panel_of(NQ * wave + f) : -1;
     soff = p >= 0 ? (uint32_t)p * (uint32_t)nst * kQ4PanelRecord + 1024u + 16u * (lane & 7) : kOob;
   }
-
-  // Always NDMA instructions, so vmcnt counts stay exact (stages past the end reload
-  // stage 0). kCheck: the stage may be the half stage of an odd block count.
   auto issue = [&](auto H, auto J, int st, auto kCheck) __attribute__((always_inline)) {
-    const int sst = st < nst ? st : 0;
     char *slot = slot_ptr(H, J);
+    const int sst = st < nst ? st : 0;
     bool half = false;
     if constexpr (decltype(kCheck)::value) half = (2 * sst + 1 == nb);
 #pragma unroll
@@ -338,7 +351,50 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   // One stage in slot J of half H. kCheck: the stage or the one it prefetches may be
   // the half stage. An inactive stage (past the half's range) only keeps the ring and the
   // barrier count in step.
-  auto stage = [&](auto H, auto J, int st, auto kCheck, bool active) __attribute__((always_inline)) {
+  // The next tile's stage nsst into slot J (persistent mode, one segment, no split, even
+  // block count): the same offsets as issue's, for the next tile's rows and panels.
+  uint32_t nxoff[NX], nqoff[NQ], nsoff;
+  auto issue_next = [&](auto J, int nsst) __attribute__((always_inline)) {
+    char *slot = slot_ptr(ic<0>{}, J);
+#pragma unroll
+    for (int i = 0; i < NX; i++) dma16(rx, slot + 8 * (NX * wave + i) * kBK * 2, nxoff[i], nsst * kBK * 2);
+#pragma unroll
+    for (int f = 0; f < NQ; f++) dma16(rp, slot + X_BYTES + (NQ * wave + f) * 1024, nqoff[f], nsst * kQ4PanelRecord);
+    if (lane < 8 * NQ) dma16(rp, slot + X_BYTES + Q_BYTES + NQ * wave * 128, nsoff, nsst * kQ4PanelRecord);
+  };
+  auto next_offsets = [&]() __attribute__((always_inline)) {
+    int ntm, ntn;
+    tile_of(w_item + xstep, ntm, ntn);
+    const int nm0 = ntm * BM, nc0 = ntn * OUT_BN;
+#pragma unroll
+    for (int i = 0; i < NX; i++) {
+      const int row = 8 * (NX * wave + i) + (lane >> 3);
+      const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+      const int r = nm0 + row;
+      nxoff[i] = r < a.m ? ((uint32_t)r * (uint32_t)a.ldx + 8u * chunk) * 2u : kOob;
+    }
+    auto npanel_of = [&](int g) -> int {
+      int p;
+      if constexpr (kSwiglu) {
+        const int wn = g / FN, f = g % FN;
+        const int j = nc0 / 32 + wn * (FN / 2) + (f % (FN / 2));
+        p = 2 * j + (f >= FN / 2 ? 1 : 0);
+      } else {
+        p = nc0 / 32 + g;
+      }
+      return p < npanels ? p : -1;
+    };
+#pragma unroll
+    for (int f = 0; f < NQ; f++) {
+      const int p = npanel_of(NQ * wave + f);
+      nqoff[f] = p >= 0 ? (uint32_t)p * (uint32_t)nst * kQ4PanelRecord + 16u * lane : kOob;
+    }
+    const int f = lane >> 3;
+    const int p = f < NQ ? npanel_of(NQ * wave + f) : -1;
+    nsoff = p >= 0 ? (uint32_t)p * (uint32_t)nst * kQ4PanelRecord + 1024u + 16u * (lane & 7) : kOob;
+  };
+
+  auto stage = [&](auto H, auto J, int st, auto kCheck, bool active, auto kNext) __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
     // stage st was issued NS-1 stages ago, (NS-2)*NDMA DMA instructions after it
     wait_vmcnt<(kNS - 2) * NDMA>();
@@ -346,7 +402,12 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     // reads were consumed by its MFMAs; a fenced barrier would drain every prefetch
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue(H, ic<decltype(J)::value + kNS - 1>{}, st + kNS - 1, kCheck);  // refills the slot of stage st-1
+    // refills the slot of stage st-1; in a tile's last ring cycle with kNext, with the
+    // next tile's stage J-1 (stage st-1 is its tile's last when J is 0)
+    if constexpr (decltype(kNext)::value && decltype(J)::value > 0)
+      issue_next(ic<decltype(J)::value - 1>{}, decltype(J)::value - 1);
+    else
+      issue(H, ic<decltype(J)::value + kNS - 1>{}, st + kNS - 1, kCheck);
     if (!active) return;
     const char *slot = slot_ptr(H, J);
     const _Float16 *xb = reinterpret_cast<const _Float16 *>(slot);
@@ -408,16 +469,25 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   auto run = [&](auto H) __attribute__((always_inline)) {
     const int sb = kb + decltype(H)::value * nst_h;
     const int se = min(ke, sb + nst_h);
-    static_for<kNS - 1>([&](auto J) { issue(H, J, sb + decltype(J)::value, yes{}); });
+    if (!primed) static_for<kNS - 1>([&](auto J) { issue(H, J, sb + decltype(J)::value, yes{}); });
     int lim = se - sb;
     if (nb & 1) lim = min(lim, nst - kNS - sb);  // stage nst-NS prefetches the half stage
     lim = max(lim, 0);
     int s0 = 0;
-    for (; s0 + kNS <= lim; s0 += kNS)
-      static_for<kNS>([&](auto J) { stage(H, J, sb + s0 + decltype(J)::value, no{}, true); });
+    // with a next tile (stages a multiple of NS), the last ring cycle is peeled
+    const int lim_main = (kCanPersist && has_next) ? lim - kNS : lim;
+    for (; s0 + kNS <= lim_main; s0 += kNS)
+      static_for<kNS>([&](auto J) { stage(H, J, sb + s0 + decltype(J)::value, no{}, true, no{}); });
+    if constexpr (kCanPersist) {
+      if (has_next) {
+        next_offsets();
+        static_for<kNS>([&](auto J) { stage(H, J, sb + s0 + decltype(J)::value, no{}, true, yes{}); });
+        s0 += kNS;
+      }
+    }
     static_for<2 * kNS>([&](auto J) {
       const int st = sb + s0 + decltype(J)::value;
-      if (s0 + decltype(J)::value < nst_h) stage(H, J, st, yes{}, st < se);
+      if (s0 + decltype(J)::value < nst_h) stage(H, J, st, yes{}, st < se, no{});
     });
   };
   if constexpr (KSPLIT == 1) {
@@ -431,8 +501,9 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     else if (kh == 2) run(ic<2>{});
     else run(ic<3>{});
   }
-  // no DMA may still be writing this workgroup's LDS when it exits
-  wait_vmcnt<0>();
+  // no DMA may still be writing this workgroup's LDS when it exits (a next tile's first
+  // stages stay in flight: the epilogues that allow persistence use no LDS)
+  if (!has_next) wait_vmcnt<0>();
   // Accumulator register group q (registers 4q .. 4q+3: rows 8q + 4lg .. +3 of every
   // fragment) belongs to K part q / NQO. After the combine each part holds the full sums
   // of its NQO groups in registers 0 .. 4*NQO-1 and runs the epilogue for those rows:
@@ -793,6 +864,9 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
       }
     }
   }
+  if (!has_next) break;
+  primed = true;
+  }  // work items
 }
 
 // Sum of the K splits' partials in split order (deterministic), then the real epilogue:
@@ -1029,6 +1103,21 @@ int normalize_splits(int k, int splits, int *split_stages) {
   return (nst + per - 1) / per;
 }
 
+// Workgroups of kernel K the GPU holds at once (a multiple of the XCD count), measured
+// once per kernel.
+template <auto K>
+int resident_wgs(int threads) {
+  static const int r = [threads] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, K, threads, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    return n * (device_cu_count() / kXcds) * kXcds;
+  }();
+  return r;
+}
+
 template <int FM, int FN, int NS = 3, int KSPLIT = 1, int WM = 1>
 int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   constexpr int BM = 32 * FM * WM;
@@ -1041,22 +1130,46 @@ int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   a.group_m = 4;
   if (a.epi != EPI_PART || a.splits < 1) a.splits = 1;
   a.splits = normalize_splits(a.k, a.splits, &a.split_stages);
-  const dim3 grid(a.tiles_m * a.tiles_n * a.splits), block(256 * KSPLIT);
+  // Persistent launch when the tiles outnumber the workgroups the GPU holds at once and
+  // the kernel can chain tiles: one grid of resident workgroups, a multiple of the XCD
+  // count, each running every (grid / XCDs)-th tile of its XCD's range.
+  const int nwork = a.tiles_m * a.tiles_n * a.splits;
+  const int nb = a.k / 32, nst = (nb + 1) / 2;
+  const bool chain = KSPLIT == 1 && WM == 1 && a.splits == 1 && a.nseg == 1 && nb % 2 == 0 && nst % NS == 0 &&
+                     (a.epi == EPI_SWIGLU || a.epi == EPI_F16 || a.epi == EPI_F32 || a.epi == EPI_RESID);
+  const dim3 block(256 * KSPLIT);
+  auto go = [&](auto kern, int resident) {
+    a.persist = chain && resident >= kXcds && nwork > resident;
+    hipLaunchKernelGGL(kern, dim3(a.persist ? resident : nwork), block, 0, s, a);
+  };
   switch (a.epi) {
-    case EPI_F16: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F16, KSPLIT, WM>), grid, block, 0, s, a); break;
-    case EPI_F32: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_F32, KSPLIT, WM>), grid, block, 0, s, a); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_RESID, KSPLIT, WM>), grid, block, 0, s, a); break;
+    case EPI_F16: {
+      constexpr auto k = gemm_q4_kernel<FM, FN, NS, EPI_F16, KSPLIT, WM>;
+      go(k, resident_wgs<k>(256 * KSPLIT));
+      break;
+    }
+    case EPI_F32: {
+      constexpr auto k = gemm_q4_kernel<FM, FN, NS, EPI_F32, KSPLIT, WM>;
+      go(k, resident_wgs<k>(256 * KSPLIT));
+      break;
+    }
+    case EPI_RESID: {
+      constexpr auto k = gemm_q4_kernel<FM, FN, NS, EPI_RESID, KSPLIT, WM>;
+      go(k, resident_wgs<k>(256 * KSPLIT));
+      break;
+    }
     case EPI_SWIGLU:
       if constexpr (FN % 2 == 0) {
-        hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_SWIGLU, KSPLIT, WM>), grid, block, 0, s, a);
+        constexpr auto k = gemm_q4_kernel<FM, FN, NS, EPI_SWIGLU, KSPLIT, WM>;
+        go(k, resident_wgs<k>(256 * KSPLIT));
         break;
       } else {
         return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "SwiGLU tiles pair gate and up fragments (even FN)");
       }
-    case EPI_PART: hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_PART, KSPLIT, WM>), grid, block, 0, s, a); break;
+    case EPI_PART: go(gemm_q4_kernel<FM, FN, NS, EPI_PART, KSPLIT, WM>, 0); break;
     case EPI_ROPE:
       if constexpr (WM == 1 && FN == 1) {
-        hipLaunchKernelGGL((gemm_q4_kernel<FM, FN, NS, EPI_ROPE, KSPLIT, WM>), grid, block, 0, s, a);
+        go(gemm_q4_kernel<FM, FN, NS, EPI_ROPE, KSPLIT, WM>, 0);
         break;
       } else {
         return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "the RoPE epilogue runs on 128-column tiles");

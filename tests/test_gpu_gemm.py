@@ -98,6 +98,22 @@ def test_benchmark_shapes_vs_fp32(ctx, M, name):
     assert cosine(y, ref) >= 0.9999
 
 
+@pytest.mark.parametrize("M,K,N", [(4096, 1536, 8960), (4000, 1536, 8864), (4096, 3072, 8192)])
+def test_persistent_tile_chain(ctx, M, K, N):
+    """Shapes with more 128 x 256 tiles than the GPU holds at once and k stages a
+    multiple of the 3-slot ring (24 and 48): the launch keeps only resident workgroups,
+    each running a strided run of its XCD's tiles and loading the next tile's first
+    stages under the current tile's epilogue; the second shape has ragged rows and
+    columns. Against fp32 within 1e-2."""
+    rng = np.random.default_rng(9000 + M + K + N)
+    w = S.random_q4(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    y = run_gemm(ctx, w.scales, w.quants, x, N, K, M)
+    ref = x.astype(np.float32) @ w.dequant_f32().T
+    assert max_rel_err(y, ref) <= 1e-2
+    assert cosine(y, ref) >= 0.9999
+
+
 @pytest.mark.parametrize("M", [1, 8, 37])
 def test_lm_head_shape(ctx, M):
     """LM-head GEMM K=1536, N=151936 at small M (the HBM-bound regime)."""

@@ -158,6 +158,24 @@ def test_llama_3b_layer_shapes():
     dm.release()
 
 
+def test_qwen_layer_one_ubatch_of_2048():
+    """One layer of the Qwen2.5-1.5B shape (hidden 1536, FFN 8960, 12/2 heads, head_dim
+    128, NeoX RoPE, biases; small vocab for the oracle's sake) on one 2048-token ubatch,
+    the benchmark's ubatch: the gate/up GEMM runs persistent (more tiles than resident
+    workgroups) with the SwiGLU epilogue, QKV with the fused RoPE epilogue, and the down
+    projection splits K across workgroups."""
+    cfg = S.ModelConfig(1, 1536, 8960, 12, 2, 128, 128, 2048, 1e6, 1e-6, 1)
+    dm, okv, res = run_both(cfg, 91, [2048], 2048, biases=True)
+    for g, _, _, r in res:
+        assert np.max(np.abs(g - r)) <= 1e-2 * float(np.abs(r).max())
+        assert cosine(g, r) >= 0.999
+        assert int(np.argmax(g)) == int(np.argmax(r))
+    dk, dv = dm.kv_host()
+    assert kv_within_one_step(dk[0], okv.k[0], np.arange(2048), dm.bpp)
+    assert kv_within_one_step(dv[0], okv.v[0], np.arange(2048), dm.bpp)
+    dm.release()
+
+
 def test_split_down_projection_runs_the_next_norm():
     """Two layers shaped so that the down projection (K = 4096) splits K across
     workgroups: its reduction also writes the next layer's attention RMSNorm (layer 0)
