@@ -394,10 +394,12 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     nsoff = p >= 0 ? (uint32_t)p * (uint32_t)nst * kQ4PanelRecord + 1024u + 16u * (lane & 7) : kOob;
   };
 
-  auto stage = [&](auto H, auto J, int st, auto kCheck, bool active, auto kNext) __attribute__((always_inline)) {
+  // need_wait false: the stage's slot was waited for before the previous tile's epilogue
+  // (stage 0 of a tile whose first stages the previous tile loaded).
+  auto stage = [&](auto H, auto J, int st, auto kCheck, bool active, auto kNext, bool need_wait) __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
     // stage st was issued NS-1 stages ago, (NS-2)*NDMA DMA instructions after it
-    wait_vmcnt<(kNS - 2) * NDMA>();
+    if (need_wait) wait_vmcnt<(kNS - 2) * NDMA>();
     // plain s_barrier: the slot is filled (vmcnt above) and the previous stage's LDS
     // reads were consumed by its MFMAs; a fenced barrier would drain every prefetch
     __builtin_amdgcn_s_barrier();
@@ -477,17 +479,24 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     // with a next tile (stages a multiple of NS), the last ring cycle is peeled
     const int lim_main = (kCanPersist && has_next) ? lim - kNS : lim;
     for (; s0 + kNS <= lim_main; s0 += kNS)
-      static_for<kNS>([&](auto J) { stage(H, J, sb + s0 + decltype(J)::value, no{}, true, no{}); });
+      static_for<kNS>([&](auto J) {
+        stage(H, J, sb + s0 + decltype(J)::value, no{}, true, no{}, decltype(J)::value != 0 || s0 != 0 || !primed);
+      });
     if constexpr (kCanPersist) {
       if (has_next) {
         next_offsets();
-        static_for<kNS>([&](auto J) { stage(H, J, sb + s0 + decltype(J)::value, no{}, true, yes{}); });
+        static_for<kNS>([&](auto J) {
+          stage(H, J, sb + s0 + decltype(J)::value, no{}, true, yes{}, decltype(J)::value != 0 || s0 != 0 || !primed);
+        });
         s0 += kNS;
+        // the next tile's stage 0 (NS-2 DMA groups issued after it) lands before the
+        // epilogue, so that tile's first stage waits for none of the epilogue's stores
+        wait_vmcnt<(kNS - 2) * NDMA>();
       }
     }
     static_for<2 * kNS>([&](auto J) {
       const int st = sb + s0 + decltype(J)::value;
-      if (s0 + decltype(J)::value < nst_h) stage(H, J, st, yes{}, st < se, no{});
+      if (s0 + decltype(J)::value < nst_h) stage(H, J, st, yes{}, st < se, no{}, true);
     });
   };
   if constexpr (KSPLIT == 1) {
