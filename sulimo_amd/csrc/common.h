@@ -157,7 +157,7 @@ struct GemmArgs {
   // Persistent launch (filled by the launcher): fewer workgroups than tiles, each running
   // a strided run of its XCD's tiles and loading the next tile's first stages under the
   // current tile's epilogue. One segment, no split, an even block count, stages a
-  // multiple of the ring depth, and an epilogue that uses no LDS.
+  // multiple of the ring depth, and the f16 or SwiGLU epilogue (no LDS use).
   int persist;
 };
 

@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   const int xcd = blockIdx.x % kXcds, jx = blockIdx.x / kXcds;
   const int xlo = xcd * (nwork / kXcds) + min(xcd, nwork % kXcds);
   const int xend = xlo + nwork / kXcds + (xcd < nwork % kXcds ? 1 : 0);
-  constexpr bool kCanPersist = KSPLIT == 1 && WM == 1 && (EPI == EPI_SWIGLU || EPI == EPI_F16 || EPI == EPI_F32 || EPI == EPI_RESID);
+  constexpr bool kCanPersist = KSPLIT == 1 && WM == 1 && (EPI == EPI_SWIGLU || EPI == EPI_F16);
   const int xstep = (kCanPersist && a.persist) ? (int)(gridDim.x / kXcds) : 0;
   if (xlo + jx >= xend) return;  // persistent grid wider than the XCD's range
   auto tile_of = [&](int w, int &tm, int &tn) {
@@ -1145,7 +1145,7 @@ int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   const int nwork = a.tiles_m * a.tiles_n * a.splits;
   const int nb = a.k / 32, nst = (nb + 1) / 2;
   const bool chain = KSPLIT == 1 && WM == 1 && a.splits == 1 && a.nseg == 1 && nb % 2 == 0 && nst % NS == 0 &&
-                     (a.epi == EPI_SWIGLU || a.epi == EPI_F16 || a.epi == EPI_F32 || a.epi == EPI_RESID);
+                     (a.epi == EPI_SWIGLU || a.epi == EPI_F16);
   const dim3 block(256 * KSPLIT);
   auto go = [&](auto kern, int resident) {
     a.persist = chain && resident >= kXcds && nwork > resident;
