@@ -224,11 +224,13 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   // major, then tiles), and the tile order walks group_m tile rows at a time, so the
   // workgroups resident on one XCD share their X rows and weight rows in its L2. Any
   // XCD count gives the same work items.
-  // Persistent mode (a.persist_wgs workgroups, one-part tiles of one segment, no split,
-  // an even block count and stages a multiple of NS): a workgroup runs every
-  // (workgroups per XCD)-th item of its XCD's range, and the last NS-1 refills of a tile
-  // load the next tile's first NS-1 stages into the same ring slots, so they land under
-  // the epilogue. Otherwise a workgroup runs one item.
+  // Persistent mode (a.persist set by the launcher: a grid of resident workgroups,
+  // one-part tiles of one segment, no split, an even block count, stages a multiple of
+  // NS, the f16 or SwiGLU epilogue): a workgroup runs every (workgroups per XCD)-th item
+  // of its XCD's range, and the last NS-1 refills of a tile load the next tile's first
+  // NS-1 stages into the same ring slots, so they land under the epilogue. Otherwise a
+  // workgroup runs one item. The loop over items below spans the rest of the kernel
+  // body (not indented).
   const int ntiles = a.tiles_m * a.tiles_n;
   const int nwork = ntiles * a.splits;
   const int xcd = blockIdx.x % kXcds, jx = blockIdx.x / kXcds;
