@@ -98,13 +98,14 @@ def test_benchmark_shapes_vs_fp32(ctx, M, name):
     assert cosine(y, ref) >= 0.9999
 
 
-@pytest.mark.parametrize("M,K,N", [(4096, 1536, 8960), (4000, 1536, 8864), (4096, 3072, 8192)])
+@pytest.mark.parametrize("M,K,N", [(4096, 1536, 8960), (4000, 1536, 8864), (4096, 3072, 8192), (1920, 1536, 8960)])
 def test_persistent_tile_chain(ctx, M, K, N):
-    """Shapes with more 128 x 256 tiles than the GPU holds at once and k stages a
-    multiple of the 3-slot ring (24 and 48): the launch keeps only resident workgroups,
-    each running a strided run of its XCD's tiles and loading the next tile's first
-    stages under the current tile's epilogue; the second shape has ragged rows and
-    columns. Against fp32 within 1e-2."""
+    """Shapes with more tiles than the GPU holds at once and k stages a multiple of the
+    3-slot ring (24 and 48): the launch keeps only resident workgroups, each running a
+    strided run of its XCD's tiles and loading the next tile's first stages under the
+    current tile's epilogue. The second shape has ragged rows and columns; the last has
+    only slightly more tiles than resident workgroups and XCD ranges of unequal length,
+    so most workgroups run one tile and a few chain two. Against fp32 within 1e-2."""
     rng = np.random.default_rng(9000 + M + K + N)
     w = S.random_q4(rng, N, K)
     x = rng.standard_normal((M, K)).astype(np.float16)
