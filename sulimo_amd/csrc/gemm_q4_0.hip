@@ -937,7 +937,11 @@ __global__ __launch_bounds__(256) void split_reduce_norm_kernel(GemmArgs a) {
   const size_t plane = (size_t)a.m * a.ldp;
   const float *p = a.part + (size_t)row * a.ldp;
   float *x = reinterpret_cast<float *>(seg.out) + (size_t)row * seg.ldo;
-  float4 xv[V];
+  // the norm weights are loaded first: loaded between the stores at the end, each load
+  // would wait for the stores before it (loads and stores retire in issue order)
+  float4 xv[V], nw[V];
+#pragma unroll
+  for (int j = 0; j < V; j++) nw[j] = *reinterpret_cast<const float4 *>(a.norm_w + 4 * min(tid + 256 * j, n4 - 1));
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < V; j++) {
@@ -977,7 +981,7 @@ __global__ __launch_bounds__(256) void split_reduce_norm_kernel(GemmArgs a) {
   for (int j = 0; j < V; j++) {
     const int c4 = tid + 256 * j;
     if (c4 >= n4) continue;
-    const float4 w = *reinterpret_cast<const float4 *>(a.norm_w + 4 * c4);
+    const float4 w = nw[j];
     const float4 nx = xv[j];
     *reinterpret_cast<half4v *>(reinterpret_cast<_Float16 *>(a.norm_out) + (size_t)row * seg.n + 4 * c4) =
         half4v{(_Float16)(nx.x * scale * w.x), (_Float16)(nx.y * scale * w.y), (_Float16)(nx.z * scale * w.z),

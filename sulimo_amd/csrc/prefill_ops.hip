@@ -45,19 +45,23 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const T *__restrict__ 
   const int lane = threadIdx.x & 63;
   if (row >= n) return;
   const T *xr = x + (size_t)row * D;
-  float4 v[V];
+  // the weights are loaded with the row: loaded between the stores, each load would
+  // wait for the stores before it (loads and stores retire in issue order)
+  float4 v[V], wl[V];
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < V; j++) {
     v[j] = load4(xr, 256 * j + 4 * lane);
-    ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    wl[j] = *reinterpret_cast<const float4 *>(w + 256 * j + 4 * lane);
   }
+#pragma unroll
+  for (int j = 0; j < V; j++) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
   ss = wave_sum(ss);
   const float scale = 1.0f / sqrtf(ss / (float)D + eps);
 #pragma unroll
   for (int j = 0; j < V; j++) {
     const int i = 256 * j + 4 * lane;
-    const float4 wv = *reinterpret_cast<const float4 *>(w + i);
+    const float4 wv = wl[j];
     const half4v o = {(_Float16)(v[j].x * scale * wv.x), (_Float16)(v[j].y * scale * wv.y),
                       (_Float16)(v[j].z * scale * wv.z), (_Float16)(v[j].w * scale * wv.w)};
     *reinterpret_cast<half4v *>(out + (size_t)row * D + i) = o;
