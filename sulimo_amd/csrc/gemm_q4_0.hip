@@ -786,6 +786,26 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   const int qj = lane & 3;
   const int cq = 4 * (l32 >> 2);  // first column of the lane's 4 after the transpose
   const bool vec_ok = ((seg.ldo | seg.col0) & 3) == 0 && ((uintptr_t)seg.out & 15) == 0;
+  // Residual epilogue of a small tile: every residual value of the vector path is loaded
+  // before the first store (a load issued after a store waits for it: loads and stores
+  // retire in issue order). Lanes outside the vector path read the row's first element
+  // and load again in the element-wise path.
+  constexpr bool kOldFirst = EPI == EPI_RESID && FM * NQO * FN <= 8;
+  float4 rold[kOldFirst ? FM : 1][kOldFirst ? NQO : 1][kOldFirst ? FN : 1];
+  if constexpr (kOldFirst) {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int lq = 0; lq < NQO; lq++)
+#pragma unroll
+        for (int f = 0; f < FN; f++) {
+          const int row = m0 + 32 * (FM * wave_m + i) + 8 * (qbase + lq) + 4 * lg + qj;
+          const int col = c0 + wave_n * 32 * FN + 32 * f + cq;
+          const bool ok = vec_ok && row < a.m && col + 4 <= seg.n;
+          const float *src = reinterpret_cast<const float *>(seg.out) + (ok ? (size_t)row * seg.ldo + seg.col0 + col : 0);
+          rold[i][lq][f] = *reinterpret_cast<const float4 *>(src);
+        }
+  }
 #pragma unroll
   for (int i = 0; i < FM; i++) {
 #pragma unroll
@@ -861,7 +881,9 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
               if (vec) {
                 float4 w = o;
                 if constexpr (EPI == EPI_RESID) {
-                  const float4 old = *reinterpret_cast<const float4 *>(dst);
+                  float4 old;
+                  if constexpr (kOldFirst) old = rold[i][lq][f];
+                  else old = *reinterpret_cast<const float4 *>(dst);
                   w = float4{old.x + o.x, old.y + o.y, old.z + o.z, old.w + o.w};
                 }
                 *reinterpret_cast<float4 *>(dst) = w;
