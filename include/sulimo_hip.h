@@ -176,7 +176,9 @@ int32_t sulimo_hip_enqueue_logits_final(sulimo_hip_ctx *ctx, const sulimo_hip_bu
                                         const sulimo_hip_buffer *quants, sulimo_hip_buffer *logits,
                                         size_t vocab_size, size_t embd_dim, size_t token_idx);
 /* wait_event_zero_spin (crates/sulimo-ocl/src/waiter.rs:39-82): blocks until the
- * stream drains with a blocking-sync event (the thread sleeps, no spin). Reports an
+ * stream drains. The calling thread sleeps on a condition variable that a HIP host
+ * function queued behind the work signals (the reference's event callback + park);
+ * it does not spin while the GPU runs. Reports an
  * asynchronous kernel failure as SULIMO_HIP_ERR_EXECUTION_FAILED. */
 int32_t sulimo_hip_wait(sulimo_hip_ctx *ctx);
 /* gemm_q4_0_f16 (crates/sulimo-ocl/src/gemm.rs:28-102): one GEMM, waited, timed. */
@@ -264,11 +266,19 @@ int32_t sulimo_hip_execute_prefill_ubatch(sulimo_hip_ctx *ctx, const sulimo_hip_
                                           sulimo_hip_prefill_scratch *scratch, size_t start_pos,
                                           size_t n);
 
-/* Optional outputs of a prefill for validation (no reference counterpart; the
- * engine's CPU prefill computes logits for every token, engine.rs:287-319). */
+/* Optional outputs and switches of a prefill for validation (no reference
+ * counterpart; the engine's CPU prefill computes logits for every token,
+ * engine.rs:287-319). */
 typedef struct {
   sulimo_hip_buffer *logits_all; /* f32 [n][vocab], or NULL */
   sulimo_hip_buffer *argmax_all; /* int32 [n] per-position top-1 token, or NULL */
+  /* Nonzero: every op of prefill.rs:362-536 runs as its own kernel, as the reference
+   * enqueues them: the q/k/v, o, gate, up and down GEMMs store f16, followed by the
+   * separate RoPE + Q8_0 store, SwiGLU, residual add and RMSNorm kernels, instead of
+   * those steps running in GEMM epilogues and the K-split reduction. The arithmetic
+   * of each step is the same; scratch.ffn_gate, ffn_up and ffn_down (f16 [n][ffn],
+   * [n][ffn], [n][embd]) must then be given. */
+  int32_t unfused;
 } sulimo_hip_prefill_outputs;
 
 /* execute_prefill_ubatch plus the per-position outputs above. */

@@ -101,6 +101,7 @@ def _declare(L):
         "orc_attention_prefill_f32": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I]),
         "orc_lookup_token_embedding_f16": (None, [_P, _P, _SZ, C.c_uint32, _P]),
         "orc_forward_token": (_I, [C.POINTER(OrcModel), C.POINTER(OrcKv), C.c_uint32, _SZ, _P]),
+        "orc_forward_token_mt": (_I, [C.POINTER(OrcModel), C.POINTER(OrcKv), C.c_uint32, _SZ, _P, _I]),
         "orc_prefill_reference": (_I, [C.POINTER(OrcModel), C.POINTER(OrcKv), _P, _SZ, _SZ, _I,
                                        _P, _P]),
     }
@@ -340,10 +341,14 @@ class OracleKv:
         self.s = OrcKv(self._kp, self._vp, capacity)
 
 
-def forward_token(om: OracleModel, kv: OracleKv, token: int, pos: int) -> np.ndarray:
-    """forward_pass.rs:190-417: f32 logits of one token (single core)."""
+def forward_token(om: OracleModel, kv: OracleKv, token: int, pos: int, threads: int = 1) -> np.ndarray:
+    """forward_pass.rs:190-417: f32 logits of one token. threads = 1 is the reference's
+    single-core path; more threads split every matvec's rows (bit-identical result)."""
     out = np.zeros(om.cfg.vocab, np.float32)
-    rc = lib().orc_forward_token(C.byref(om.model), C.byref(kv.s), token, pos, _p(out))
+    if threads == 1:
+        rc = lib().orc_forward_token(C.byref(om.model), C.byref(kv.s), token, pos, _p(out))
+    else:
+        rc = lib().orc_forward_token_mt(C.byref(om.model), C.byref(kv.s), token, pos, _p(out), threads)
     if rc:
         raise MemoryError("orc_forward_token failed")
     return out

@@ -254,6 +254,22 @@ void orc_matvec_q4_0_q8_0_avx2(const uint8_t *w_scales, const uint8_t *w_quants,
                                         bpr);
 }
 
+/* The same rows split over `threads` OpenMP threads, as ThreadPool::execute_parallel
+ * splits matvec rows (crates/sulimo-cpu/src/thread_pool.rs:98-126). Each row is one
+ * independent dot, so the result equals the single-thread matvec bit for bit. */
+static void matvec_threads(const uint8_t *w_scales, const uint8_t *w_quants, const uint8_t *x_q8,
+                           size_t rows, size_t cols, float *out, int threads) {
+  if (threads <= 1) {
+    orc_matvec_q4_0_q8_0_avx2(w_scales, w_quants, x_q8, rows, cols, out);
+    return;
+  }
+  size_t bpr = cols / 32;
+#pragma omp parallel for schedule(static) num_threads(threads)
+  for (size_t r = 0; r < rows; r++)
+    out[r] = orc_vec_dot_q4_0_q8_0_avx2(w_scales + r * bpr * 2, w_quants + r * bpr * 16, x_q8,
+                                        bpr);
+}
+
 /* rmsnorm_scalar, scalar.rs:23-38. */
 void orc_rmsnorm_scalar(const float *x, const float *w, float eps, size_t n, float *out) {
   float sum_sq = 0.0f;
@@ -503,6 +519,13 @@ static void head_norms(const float *w, float *v, size_t heads, size_t hd, float 
 }
 
 int orc_forward_token(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos, float *logits) {
+  return orc_forward_token_mt(m, kv, token, pos, logits, 1);
+}
+
+/* forward_token with its matvecs' rows split over `threads` threads (1 = the
+ * reference's single-core path, forward_pass.rs:197 leaves its pool unused). */
+int orc_forward_token_mt(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos, float *logits,
+                         int threads) {
   const orc_config *c = &m->cfg;
   size_t D = c->embd, F = c->ffn, hd = c->head_dim;
   size_t qd = (size_t)c->n_head * hd, kvd = (size_t)c->n_head_kv * hd;
@@ -527,9 +550,9 @@ int orc_forward_token(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos
     const orc_layer *L = &m->layers[l];
     orc_rmsnorm_avx2(x, L->attn_norm, c->eps, D, h);
     orc_quantize_f32_to_q8_0(h, D, q8);
-    orc_matvec_q4_0_q8_0_avx2(L->q.scales, L->q.quants, q8, qd, D, q);
-    orc_matvec_q4_0_q8_0_avx2(L->k.scales, L->k.quants, q8, kvd, D, k);
-    orc_matvec_q4_0_q8_0_avx2(L->v.scales, L->v.quants, q8, kvd, D, v);
+    matvec_threads(L->q.scales, L->q.quants, q8, qd, D, q, threads);
+    matvec_threads(L->k.scales, L->k.quants, q8, kvd, D, k, threads);
+    matvec_threads(L->v.scales, L->v.quants, q8, kvd, D, v, threads);
     add_bias(L->q_bias, q, qd);
     add_bias(L->k_bias, k, kvd);
     add_bias(L->v_bias, v, kvd);
@@ -547,20 +570,20 @@ int orc_forward_token(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos
     orc_causal_gqa_decode_scalar(q, kv->k[l], kv->v[l], bpp, cap, pos + 1 - ctx, ctx,
                                  c->n_head, c->n_head_kv, hd, scores, deq, ao);
     orc_quantize_f32_to_q8_0(ao, qd, q8);
-    orc_matvec_q4_0_q8_0_avx2(L->o.scales, L->o.quants, q8, D, qd, h);
+    matvec_threads(L->o.scales, L->o.quants, q8, D, qd, h, threads);
     for (size_t i = 0; i < D; i++) x[i] += h[i];
     orc_rmsnorm_avx2(x, L->ffn_norm, c->eps, D, h);
     orc_quantize_f32_to_q8_0(h, D, q8);
-    orc_matvec_q4_0_q8_0_avx2(L->gate.scales, L->gate.quants, q8, F, D, g);
-    orc_matvec_q4_0_q8_0_avx2(L->up.scales, L->up.quants, q8, F, D, u);
+    matvec_threads(L->gate.scales, L->gate.quants, q8, F, D, g, threads);
+    matvec_threads(L->up.scales, L->up.quants, q8, F, D, u, threads);
     orc_swiglu_scalar(g, u, F, sw);
     orc_quantize_f32_to_q8_0(sw, F, q8f);
-    orc_matvec_q4_0_q8_0_avx2(L->down.scales, L->down.quants, q8f, D, F, dn);
+    matvec_threads(L->down.scales, L->down.quants, q8f, D, F, dn, threads);
     for (size_t i = 0; i < D; i++) x[i] += dn[i];
   }
   orc_rmsnorm_avx2(x, m->output_norm, c->eps, D, h);
   orc_quantize_f32_to_q8_0(h, D, q8);
-  orc_matvec_q4_0_q8_0_avx2(m->output.scales, m->output.quants, q8, c->vocab, D, logits);
+  matvec_threads(m->output.scales, m->output.quants, q8, c->vocab, D, logits, threads);
 done:
   free(x); free(h); free(q); free(k); free(v); free(ao); free(g); free(u); free(sw); free(dn);
   free(scores); free(deq); free(q8); free(q8f);
@@ -623,43 +646,60 @@ int orc_prefill_reference(const orc_model *m, orc_kv *kv, const uint16_t *x_in, 
       orc_quantize_f32_to_q8_0(v + t * kvd, kvd, nv + t * bpp);
     }
     /* attention: sliding window of the last `cap` positions; positions before
-     * start_pos come from the ring, new ones from this ubatch's staged codes */
-#pragma omp parallel
+     * start_pos come from the ring, new ones from this ubatch's staged codes. The
+     * window's K/V rows are dequantized once per layer (Q8_0 dequantization is exact,
+     * code * f32(d)), so every score and output sum sees the values and the order
+     * of causal_gqa_decode_scalar. */
     {
-      float *scores = malloc(cap * 4), *deq = malloc(hd * 4);
-      size_t hpk = (size_t)c->n_head / c->n_head_kv;
-      float scale = 1.0f / sqrtf((float)hd);
-      size_t hb = (hd / 32) * 34;
+      size_t lo = start_pos + 1 > cap ? start_pos + 1 - cap : 0;
+      size_t span = start_pos + n - lo;
+      float *kf = malloc(span * kvd * 4), *vf = malloc(span * kvd * 4);
+      if (!kf || !vf) {
+        free(kf);
+        free(vf);
+        rc = -1;
+        break;
+      }
+#pragma omp parallel for schedule(static)
+      for (size_t p = lo; p < start_pos + n; p++) {
+        const uint8_t *kp = p < start_pos ? kv->k[l] + (p % cap) * bpp : nk + (p - start_pos) * bpp;
+        const uint8_t *vp = p < start_pos ? kv->v[l] + (p % cap) * bpp : nv + (p - start_pos) * bpp;
+        orc_dequant_q8_0(kp, kvd / 32, kf + (p - lo) * kvd);
+        orc_dequant_q8_0(vp, kvd / 32, vf + (p - lo) * kvd);
+      }
+#pragma omp parallel
+      {
+        float *scores = malloc(cap * 4);
+        size_t hpk = (size_t)c->n_head / c->n_head_kv;
+        float scale = 1.0f / sqrtf((float)hd);
 #pragma omp for schedule(dynamic, 4)
-      for (size_t t = 0; t < n; t++) {
-        if (!scores || !deq) continue;
-        size_t P = start_pos + t;
-        size_t ctx = P + 1 < cap ? P + 1 : cap;
-        size_t first = P + 1 - ctx;
-        for (int hh = 0; hh < c->n_head; hh++) {
-          size_t kvh = hh / hpk;
-          const float *qh = q + t * qd + hh * hd;
-          for (size_t j = 0; j < ctx; j++) {
-            size_t p = first + j;
-            const uint8_t *kp = p < start_pos ? kv->k[l] + (p % cap) * bpp : nk + (p - start_pos) * bpp;
-            orc_dequant_q8_0(kp + kvh * hb, hd / 32, deq);
-            float dot = 0.0f;
-            for (size_t d = 0; d < hd; d++) dot += qh[d] * deq[d];
-            scores[j] = dot * scale;
-          }
-          orc_softmax_scalar(scores, ctx);
-          float *oh = ao + t * qd + hh * hd;
-          for (size_t d = 0; d < hd; d++) oh[d] = 0.0f;
-          for (size_t j = 0; j < ctx; j++) {
-            size_t p = first + j;
-            const uint8_t *vp = p < start_pos ? kv->v[l] + (p % cap) * bpp : nv + (p - start_pos) * bpp;
-            orc_dequant_q8_0(vp + kvh * hb, hd / 32, deq);
-            for (size_t d = 0; d < hd; d++) oh[d] += scores[j] * deq[d];
+        for (size_t t = 0; t < n; t++) {
+          if (!scores) continue;
+          size_t P = start_pos + t;
+          size_t ctx = P + 1 < cap ? P + 1 : cap;
+          size_t first = P + 1 - ctx;
+          for (int hh = 0; hh < c->n_head; hh++) {
+            size_t kvh = hh / hpk;
+            const float *qh = q + t * qd + hh * hd;
+            for (size_t j = 0; j < ctx; j++) {
+              const float *kr = kf + (first + j - lo) * kvd + kvh * hd;
+              float dot = 0.0f;
+              for (size_t d = 0; d < hd; d++) dot += qh[d] * kr[d];
+              scores[j] = dot * scale;
+            }
+            orc_softmax_scalar(scores, ctx);
+            float *oh = ao + t * qd + hh * hd;
+            for (size_t d = 0; d < hd; d++) oh[d] = 0.0f;
+            for (size_t j = 0; j < ctx; j++) {
+              const float *vr = vf + (first + j - lo) * kvd + kvh * hd;
+              for (size_t d = 0; d < hd; d++) oh[d] += scores[j] * vr[d];
+            }
           }
         }
+        free(scores);
       }
-      free(scores);
-      free(deq);
+      free(kf);
+      free(vf);
     }
     for (size_t t = 0; t < n; t++) {
       memcpy(kv->k[l] + ((start_pos + t) % cap) * bpp, nk + t * bpp, bpp);

@@ -145,6 +145,8 @@ typedef struct {
  * vocab logits.
  * Returns 0, or -1 when a scratch allocation fails. */
 int orc_forward_token(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos, float *logits);
+int orc_forward_token_mt(const orc_model *m, orc_kv *kv, uint32_t token, size_t pos, float *logits,
+                         int threads);
 
 /* fp32 reference prefill in the device op order of execute_prefill_ubatch
  * (crates/sulimo-ocl/src/prefill.rs:362-560) with the rounding points of the

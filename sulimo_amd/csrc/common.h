@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <condition_variable>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -21,17 +23,36 @@ struct ProfRecord {
 // ---------------------------------------------------------------------------
 // Host-side objects behind the opaque C handles
 // ---------------------------------------------------------------------------
+// Where a waiting engine thread sleeps until a host function on the context's waiter
+// stream wakes it (posted counts the wake-ups).
+struct ParkSlot {
+  std::mutex m;
+  std::condition_variable cv;
+  uint64_t posted = 0;
+};
+
 struct sulimo_hip_ctx {
   int device = 0;
   bool shared = false;  // the get_or_init singleton (never freed)
   hipStream_t stream = nullptr;
-  hipEvent_t done_event = nullptr;  // blocking-sync event used by sulimo_hip_wait
+  hipEvent_t done_event = nullptr;  // end of the queued work, recorded by every wait
+  // Zero-spin waiting: a host function on `side` (gated on an event of `stream`)
+  // wakes the thread parked in `park`; near_event marks a point shortly before the
+  // end of a prefill, so that the wake-up latency of the host function overlaps the
+  // last kernels.
+  hipStream_t side = nullptr;
+  hipEvent_t near_event = nullptr;
+  ParkSlot park;
+  uint64_t park_want = 0;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   sulimo_hip_device_info info{};
   // Prefill workspace (grown on demand): f32 residual stream, Q8_0 K/V staging
   // for ring-wrapping ubatches, per-row argmax partials.
   void *ws = nullptr;
   size_t ws_bytes = 0;
+  // Token ids staged for sulimo_hip_embed_tokens (grown on demand).
+  void *tok = nullptr;
+  size_t tok_bytes = 0;
   // Per-launch event timing (sulimo_hip_set_profiling).
   bool prof = false;
   std::vector<hipEvent_t> ev_pool;  // pairs: [2i] start, [2i+1] end
@@ -169,6 +190,25 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done = nul
 // Partial-sum workspace launch_gemm_q4_0 would use for this GEMM given unlimited room.
 size_t gemm_q4_0_workspace_bytes(const GemmArgs &a);
 
+// Blocks the calling thread until all work queued on ctx->stream is done, without
+// spinning while the GPU runs: the thread sleeps until a host function enqueued after
+// `gate` (an event already recorded on ctx->stream; null = the end of the queue)
+// wakes it, then waits for the rest of the queue. Reports asynchronous failures.
+int32_t wait_parked(sulimo_hip_ctx *ctx, hipEvent_t gate);
+
+// The RoPE rotation terms a*b - c*d and a*b + c*d with both products rounded to f32
+// before the add (no fused multiply-add), as the reference's rope_f16 and
+// rope_head_scalar compute them; every kernel that rotates uses these, so the fused
+// and the separate RoPE give identical bits.
+__device__ __forceinline__ float rot_sub(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+  return a * b - c * d;
+}
+__device__ __forceinline__ float rot_add(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+  return a * b + c * d;
+}
+
 // Compute units of the current device (cached per device).
 int device_cu_count();
 
@@ -201,6 +241,7 @@ int32_t launch_silu_mul(const uint16_t *g, const uint16_t *u, uint16_t *out, siz
                         hipStream_t s);
 int32_t launch_add_f16(uint16_t *a, const uint16_t *b, size_t total, hipStream_t s);
 int32_t launch_f16_to_f32(const uint16_t *in, float *out, size_t total, hipStream_t s);
+int32_t launch_add_f16_to_f32(float *x, const uint16_t *b, size_t total, hipStream_t s);
 int32_t launch_embed_q4_0(const uint16_t *scales, const uint8_t *quants, const uint32_t *tokens,
                           int n, int embd, uint16_t *x, hipStream_t s);
 // RoPE on q (in place, f16) and k (f32 rotation), then Q8_0 of k and v into

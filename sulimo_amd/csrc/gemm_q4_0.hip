@@ -675,10 +675,10 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
             for (int j = 0; j < 4; j++) {
               if (lo) {
                 const float v0 = x[j], v1 = p[j];
-                o[f][q][j] = v0 * cc[j] - v1 * ss[j];
+                o[f][q][j] = rot_sub(v0, cc[j], v1, ss[j]);
               } else {
                 const float v0 = p[j], v1 = x[j];
-                o[f][q][j] = v0 * ss[j] + v1 * cc[j];
+                o[f][q][j] = rot_add(v0, ss[j], v1, cc[j]);
               }
             }
           } else {
@@ -686,8 +686,8 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
 #pragma unroll
             for (int j = 0; j < 4; j += 2) {
               const float v0 = x[j], v1 = x[j + 1];
-              o[f][q][j] = v0 * cc[j / 2] - v1 * ss[j / 2];
-              o[f][q][j + 1] = v0 * ss[j / 2] + v1 * cc[j / 2];
+              o[f][q][j] = rot_sub(v0, cc[j / 2], v1, ss[j / 2]);
+              o[f][q][j + 1] = rot_add(v0, ss[j / 2], v1, cc[j / 2]);
             }
           }
         }
@@ -818,9 +818,10 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            // gate and up rounded to f16 first, as their separate GEMM outputs would be
+            // gate and up rounded to f16 first, as their separate GEMM outputs would be,
+            // then silu_mul_f16's arithmetic (prefill.cl:240-253): g / (1 + e^-g) * u
             const float g = (float)(_Float16)acc[i][f][4 * lq + e], u = (float)(_Float16)acc[i][f + FN / 2][4 * lq + e];
-            v[e] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+            v[e] = g / (1.0f + expf(-g)) * u;
           }
           const uint2 o = quad_t16(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), qj);
           const int col = c0 + wave_n * 16 * FN + 32 * f + cq;

@@ -53,14 +53,6 @@ int32_t begin(sulimo_hip_ctx *ctx) {
   return SULIMO_HIP_OK;
 }
 
-// Small on-demand device buffer for token ids (separate from the workspace).
-struct TokenBuf {
-  void *p = nullptr;
-  size_t bytes = 0;
-  int device = -1;
-};
-thread_local TokenBuf g_tok;
-
 // Y[n][m] = X[n][k] W[m][k]^T for the Q4_0 matrix W = (scales, quants), through its
 // panel copy (built on first use).
 // With own_workspace, a K split may use the context workspace for its partials (only
@@ -152,7 +144,6 @@ int32_t sulimo_hip_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *s
   if ((rc = sulimo_hip_enqueue_gemm_q4_0_f16(ctx, scales, quants, x, out, m, k, n))) return rc;
   float ms = 0.0f;
   if ((rc = sulimo_hip_timer_stop(ctx, &ms))) return rc;
-  if ((rc = sulimo_hip_wait(ctx))) return rc;
   if (profile) {
     profile->duration_seconds = ms * 1e-3;
     profile->gflops = ms > 0 ? 2.0 * m * n * k / (ms * 1e-3) / 1e9 : 0.0;
@@ -292,21 +283,22 @@ int32_t sulimo_hip_embed_tokens(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *em
   NEED(embd_quants, vocab * (embd / 32) * 16, "embd_quants");
   NEED(x, n * embd * 2, "x");
   wrote(x);
-  if (g_tok.bytes < n * 4 || g_tok.device != ctx->device) {
-    if (g_tok.p) {
+  // The ids are staged in a buffer of this context, so that the copy and the gather
+  // are ordered on this context's stream (another context cannot overwrite them).
+  if (ctx->tok_bytes < n * 4) {
+    if (ctx->tok) {
       SULIMO_HIP_TRY(hipStreamSynchronize(ctx->stream));
-      hipFree(g_tok.p);
-      g_tok.p = nullptr;
-      g_tok.bytes = 0;
+      hipFree(ctx->tok);
+      ctx->tok = nullptr;
+      ctx->tok_bytes = 0;
     }
     size_t sz = ((n * 4) + 4095) & ~(size_t)4095;
-    SULIMO_HIP_TRY(hipMalloc(&g_tok.p, sz));
-    g_tok.bytes = sz;
-    g_tok.device = ctx->device;
+    SULIMO_HIP_TRY(hipMalloc(&ctx->tok, sz));
+    ctx->tok_bytes = sz;
   }
-  SULIMO_HIP_TRY(hipMemcpyAsync(g_tok.p, tokens, n * 4, hipMemcpyHostToDevice, ctx->stream));
+  SULIMO_HIP_TRY(hipMemcpyAsync(ctx->tok, tokens, n * 4, hipMemcpyHostToDevice, ctx->stream));
   return launch_embed_q4_0(dp<const uint16_t>(embd_scales), dp<const uint8_t>(embd_quants),
-                           reinterpret_cast<const uint32_t *>(g_tok.p), (int)n, (int)embd,
+                           reinterpret_cast<const uint32_t *>(ctx->tok), (int)n, (int)embd,
                            dp<uint16_t>(x), ctx->stream);
 }
 
@@ -434,6 +426,13 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   }
   if (outputs && outputs->logits_all) NEED(outputs->logits_all, n * V * 4, "logits_all");
   if (outputs && outputs->argmax_all) NEED(outputs->argmax_all, n * 4, "argmax_all");
+  // Validation mode: every op as its own kernel (no GEMM epilogue fusion).
+  const bool unfused = outputs && outputs->unfused;
+  if (unfused) {
+    NEED(scratch->ffn_gate, n * F * 2, "scratch.ffn_gate");
+    NEED(scratch->ffn_up, n * F * 2, "scratch.ffn_up");
+    NEED(scratch->ffn_down, n * D * 2, "scratch.ffn_down");
+  }
 
   // Workspace: f32 residual [n][D] | staged K codes [n][bpp] | staged V codes | argmax logits chunk.
   const bool staged = start_pos + n > cap;
@@ -490,6 +489,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   for (sulimo_hip_buffer *b : {scratch->x, scratch->h, scratch->q, scratch->k, scratch->v, scratch->attn_out,
                                scratch->ffn_swiglu, scratch->logits})
     wrote(b);
+  if (unfused)
+    for (sulimo_hip_buffer *b : {scratch->ffn_gate, scratch->ffn_up, scratch->ffn_down}) wrote(b);
   for (size_t l = 0; l < L; l++) {
     wrote(kv->k_buffers[l]);
     wrote(kv->v_buffers[l]);
@@ -557,8 +558,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     // 2. q, k, v projections as one segmented GEMM. Without QK-norm and with a full-width
     // rotation its epilogue also runs 3-4 (RoPE, Q8_0 of k and v, window entries); a
     // ubatch of at most 4 tokens takes the GEMV and the separate kernel.
-    const bool fuse_rope = !opt_f32(T.attn_q_norm) && !opt_f32(T.attn_k_norm) && cfg->rope_dim == (int)hd &&
-                           (hd == 64 || hd == 128) && n > 4;
+    const bool fuse_rope = !unfused && !opt_f32(T.attn_q_norm) && !opt_f32(T.attn_k_norm) &&
+                           cfg->rope_dim == (int)hd && (hd == 64 || hd == 128) && n > 4;
     GemmArgs g{};
     g.x = dp<const uint16_t>(scratch->h);
     g.m = in;
@@ -612,7 +613,16 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     go.norm_w = dp<const float>(T.ffn_norm);
     go.norm_out = dp<uint16_t>(scratch->h);
     go.norm_eps = cfg->eps;
-    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s, &h_ready); })))
+    if (unfused) {
+      go.epi = EPI_F16;
+      go.seg[0].out = scratch->ffn_down->dev;
+      go.norm_w = nullptr;
+      go.norm_out = nullptr;
+      h_ready = false;
+      if ((rc = launch_gemm_q4_0(go, s)) ||
+          (rc = launch_add_f16_to_f32(xres, dp<const uint16_t>(scratch->ffn_down), n * D, s)))
+        return rc;
+    } else if ((rc = timed(ctx, PROF_GEMM, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s, &h_ready); })))
       return rc;
     // 8. FFN RMSNorm
     if (!h_ready && (rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
@@ -629,7 +639,24 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     gu.epi = EPI_SWIGLU;
     gu.seg[0] = GemmSegment{pgu, scratch->ffn_swiglu->dev, (int)F, (int)F, 0};
     gu.nseg = 1;
-    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gu), gemm_bytes(gu), [&] { return launch_gemm_q4_0(gu, s); }))) return rc;
+    if (unfused) {
+      // gate and up as separate f16 GEMMs, then silu(gate) * up
+      const uint8_t *pg, *pu;
+      if ((rc = get_q4_panels(ctx, T.ffn_gate_scales, T.ffn_gate_quants, nullptr, nullptr, (int)F, (int)D, &pg)) ||
+          (rc = get_q4_panels(ctx, T.ffn_up_scales, T.ffn_up_quants, nullptr, nullptr, (int)F, (int)D, &pu)))
+        return rc;
+      gu.epi = EPI_F16;
+      gu.part = gemm_part;
+      gu.part_bytes = gemm_ws;
+      gu.seg[0] = GemmSegment{pg, scratch->ffn_gate->dev, (int)F, (int)F, 0};
+      if ((rc = launch_gemm_q4_0(gu, s))) return rc;
+      gu.seg[0] = GemmSegment{pu, scratch->ffn_up->dev, (int)F, (int)F, 0};
+      if ((rc = launch_gemm_q4_0(gu, s)) ||
+          (rc = launch_silu_mul(dp<const uint16_t>(scratch->ffn_gate), dp<const uint16_t>(scratch->ffn_up),
+                                dp<uint16_t>(scratch->ffn_swiglu), n * F, s)))
+        return rc;
+    } else if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gu), gemm_bytes(gu), [&] { return launch_gemm_q4_0(gu, s); })))
+      return rc;
     // 11-12. down projection, residual add fused
     GemmArgs gd{};
     gd.x = dp<const uint16_t>(scratch->ffn_swiglu);
@@ -642,11 +669,22 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     gd.part = gemm_part;
     gd.part_bytes = gemm_ws;
     const bool last = l + 1 == L;
+    // the wake-up of the final wait is gated here, some 50-100 us before the end
+    if (last) SULIMO_HIP_TRY(hipEventRecord(ctx->near_event, s));
     gd.norm_w = dp<const float>(last ? tensors->output_norm : tensors->layers[l + 1].attn_norm);
     gd.norm_out = dp<uint16_t>(scratch->h);
     gd.norm_x16 = last ? dp<uint16_t>(scratch->x) : nullptr;
     gd.norm_eps = cfg->eps;
-    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s, &h_ready); })))
+    if (unfused) {
+      gd.epi = EPI_F16;
+      gd.seg[0].out = scratch->ffn_down->dev;
+      gd.norm_w = nullptr;
+      gd.norm_out = gd.norm_x16 = nullptr;
+      h_ready = false;
+      if ((rc = launch_gemm_q4_0(gd, s)) ||
+          (rc = launch_add_f16_to_f32(xres, dp<const uint16_t>(scratch->ffn_down), n * D, s)))
+        return rc;
+    } else if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s, &h_ready); })))
       return rc;
   }
   // 13. output RMSNorm of all n rows (h), final residual back to scratch.x as f16
@@ -674,8 +712,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
         return rc;
     }
   }
-  // 15. one blocking wait for the whole ubatch
-  rc = sulimo_hip_wait(ctx);
+  // 15. one wait for the whole ubatch (the thread sleeps while the GPU works)
+  rc = wait_parked(ctx, ctx->near_event);
   if (ctx->prof) {
     prof_collect(ctx);
     ctx->stats.prefill_calls++;

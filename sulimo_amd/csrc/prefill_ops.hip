@@ -136,8 +136,8 @@ __global__ void rope_f16_kernel(_Float16 *vec, int head_count, int head_dim, int
   const int i0 = mode == 0 ? 2 * i : i;
   const int i1 = mode == 0 ? 2 * i + 1 : i + half;
   const float v0 = (float)hp[i0], v1 = (float)hp[i1];
-  hp[i0] = (_Float16)(v0 * c - v1 * s);
-  hp[i1] = (_Float16)(v0 * s + v1 * c);
+  hp[i0] = (_Float16)rot_sub(v0, c, v1, s);
+  hp[i1] = (_Float16)rot_add(v0, s, v1, c);
 }
 
 // Q8_0 quantization of the 32 values held by the 32 lanes of a half-wave
@@ -180,6 +180,14 @@ __global__ void add_f16_kernel(_Float16 *a, const _Float16 *b, size_t total) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   a[i] = (_Float16)((float)a[i] + (float)b[i]);
+}
+
+// The f32 residual update x += f16 value (the residual epilogue's x += f16(acc) on a
+// GEMM output already stored in f16).
+__global__ void add_f16_to_f32_kernel(float *x, const _Float16 *b, size_t total) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  x[i] += (float)b[i];
 }
 
 __global__ void f16_to_f32_kernel(const _Float16 *in, float *out, size_t total) {
@@ -247,8 +255,8 @@ __global__ __launch_bounds__(256) void rope_qkv_store_kernel(
       const int i0 = mode == 0 ? 2 * i : i;
       const int i1 = mode == 0 ? 2 * i + 1 : i + half;
       const float v0 = buf[i0], v1 = buf[i1];
-      buf[i0] = v0 * c - v1 * s;
-      buf[i1] = v0 * s + v1 * c;
+      buf[i0] = rot_sub(v0, c, v1, s);
+      buf[i1] = rot_add(v0, s, v1, c);
     }
     __builtin_amdgcn_wave_barrier();
     if (hs < n_head) {
@@ -334,8 +342,8 @@ __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
         const float2 r = cs[(e0 + j) / 2];
         const float c = r.x, s = r.y;
         const float v0 = xf[j], v1 = xf[j + 1];
-        o[j] = v0 * c - v1 * s;
-        o[j + 1] = v0 * s + v1 * c;
+        o[j] = rot_sub(v0, c, v1, s);
+        o[j + 1] = rot_add(v0, s, v1, c);
       }
     } else {  // pairs (i, i + half): the partner unit is half away
 #pragma unroll
@@ -344,10 +352,10 @@ __global__ __launch_bounds__(256) void rope_qkv_store_vec_kernel(
         const float c = r.x, s = r.y;
         if (lo) {
           const float v0 = xf[j], v1 = pf[j];
-          o[j] = v0 * c - v1 * s;
+          o[j] = rot_sub(v0, c, v1, s);
         } else {
           const float v0 = pf[j], v1 = xf[j];
-          o[j] = v0 * s + v1 * c;
+          o[j] = rot_add(v0, s, v1, c);
         }
       }
     }
@@ -524,6 +532,13 @@ int32_t launch_add_f16(uint16_t *a, const uint16_t *b, size_t total, hipStream_t
                      reinterpret_cast<_Float16 *>(a), reinterpret_cast<const _Float16 *>(b),
                      total);
   return check_launch("add_f16_kernel");
+}
+
+int32_t launch_add_f16_to_f32(float *x, const uint16_t *b, size_t total, hipStream_t s) {
+  if (total == 0) return SULIMO_HIP_OK;
+  hipLaunchKernelGGL(add_f16_to_f32_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, s, x,
+                     reinterpret_cast<const _Float16 *>(b), total);
+  return check_launch("add_f16_to_f32_kernel");
 }
 
 int32_t launch_f16_to_f32(const uint16_t *in, float *out, size_t total, hipStream_t s) {

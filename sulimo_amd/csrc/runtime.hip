@@ -122,13 +122,59 @@ static int32_t create_ctx(int device, bool shared, sulimo_hip_ctx **out) {
     return fail(SULIMO_HIP_ERR_BUILD_FAILED, m);
   }
   if ((e = hipSetDevice(device)) != hipSuccess || (e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
-      (e = hipEventCreateWithFlags(&c->done_event, hipEventBlockingSync | hipEventDisableTiming)) != hipSuccess ||
+      (e = hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&c->done_event, hipEventDisableTiming)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&c->near_event, hipEventDisableTiming)) != hipSuccess ||
       (e = hipEventCreate(&c->t0)) != hipSuccess || (e = hipEventCreate(&c->t1)) != hipSuccess) {
     int32_t r = hip_fail(e, "context creation");
     delete c;
     return r;
   }
   *out = c;
+  return SULIMO_HIP_OK;
+}
+
+// Host function run by the HIP runtime on the waiter stream.
+static void park_post(void *p) {
+  ParkSlot *k = static_cast<ParkSlot *>(p);
+  std::lock_guard<std::mutex> g(k->m);
+  k->posted++;
+  k->cv.notify_all();
+}
+
+// The reference parks the engine thread until an OpenCL event callback unparks it
+// (crates/sulimo-ocl/src/waiter.rs:25-82). HIP's own synchronization calls spin on
+// the completion signal for their whole duration (a core at 100 % while the GPU
+// runs), so the park is built the same way here: a host function (hipLaunchHostFunc)
+// notifies a condition variable. It runs some 70 us after the work before it, so a
+// gate placed a little before the end of the work (near_event) hides that latency;
+// that host function goes on the second stream, behind the gate, so that the work
+// stream does not stall on it. Without a gate it goes on the work stream itself (a
+// cross-stream wait costs some 20 us of CPU), where nothing follows it. The final
+// hipEventSynchronize spins only over what is left after the wake-up.
+int32_t wait_parked(sulimo_hip_ctx *ctx, hipEvent_t gate) {
+  SULIMO_HIP_TRY(hipSetDevice(ctx->device));
+  SULIMO_HIP_TRY(hipEventRecord(ctx->done_event, ctx->stream));
+  if (hipEventQuery(ctx->done_event) == hipErrorNotReady) {
+    const uint64_t want = ++ctx->park_want;
+    hipError_t e = hipSuccess;
+    hipStream_t hs = ctx->stream;
+    if (gate) {
+      hs = ctx->side;
+      e = hipStreamWaitEvent(ctx->side, gate, 0);
+    }
+    if (e == hipSuccess) e = hipLaunchHostFunc(hs, park_post, &ctx->park);
+    if (e == hipSuccess) {
+      std::unique_lock<std::mutex> l(ctx->park.m);
+      ctx->park.cv.wait(l, [&] { return ctx->park.posted >= want; });
+    } else {
+      ctx->park_want--;  // no host function queued: fall back to the runtime's wait
+    }
+  }
+  hipError_t e = hipEventSynchronize(ctx->done_event);
+  if (e != hipSuccess) return hip_fail(e, "stream execution");
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "stream execution");
   return SULIMO_HIP_OK;
 }
 
@@ -164,11 +210,15 @@ int32_t sulimo_hip_context_release(sulimo_hip_ctx *ctx) {
   hipSetDevice(ctx->device);
   hipStreamSynchronize(ctx->stream);
   if (ctx->ws) hipFree(ctx->ws);
+  if (ctx->tok) hipFree(ctx->tok);
+  hipStreamSynchronize(ctx->side);
   hipEventDestroy(ctx->done_event);
+  hipEventDestroy(ctx->near_event);
   hipEventDestroy(ctx->t0);
   hipEventDestroy(ctx->t1);
   for (hipEvent_t e : ctx->ev_pool) hipEventDestroy(e);
   hipStreamDestroy(ctx->stream);
+  hipStreamDestroy(ctx->side);
   delete ctx;
   return SULIMO_HIP_OK;
 }
@@ -205,13 +255,7 @@ int32_t sulimo_hip_probe(sulimo_hip_probe_result *out) {
 
 int32_t sulimo_hip_wait(sulimo_hip_ctx *ctx) {
   if (!ctx) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "ctx is null");
-  SULIMO_HIP_TRY(hipSetDevice(ctx->device));
-  SULIMO_HIP_TRY(hipEventRecord(ctx->done_event, ctx->stream));
-  hipError_t e = hipEventSynchronize(ctx->done_event);
-  if (e != hipSuccess) return hip_fail(e, "stream execution");
-  e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "stream execution");
-  return SULIMO_HIP_OK;
+  return wait_parked(ctx, nullptr);
 }
 
 int32_t sulimo_hip_set_profiling(sulimo_hip_ctx *ctx, int32_t enable) {
@@ -239,7 +283,8 @@ int32_t sulimo_hip_timer_start(sulimo_hip_ctx *ctx) {
 int32_t sulimo_hip_timer_stop(sulimo_hip_ctx *ctx, float *elapsed_ms) {
   if (!ctx || !elapsed_ms) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "null argument");
   SULIMO_HIP_TRY(hipEventRecord(ctx->t1, ctx->stream));
-  SULIMO_HIP_TRY(hipEventSynchronize(ctx->t1));
+  int32_t rc = wait_parked(ctx, nullptr);
+  if (rc) return rc;
   SULIMO_HIP_TRY(hipEventElapsedTime(elapsed_ms, ctx->t0, ctx->t1));
   return SULIMO_HIP_OK;
 }

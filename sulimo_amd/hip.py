@@ -122,7 +122,7 @@ class PrefillScratchC(C.Structure):
 
 
 class PrefillOutputsC(C.Structure):
-    _fields_ = [("logits_all", _BP), ("argmax_all", _BP)]
+    _fields_ = [("logits_all", _BP), ("argmax_all", _BP), ("unfused", C.c_int32)]
 
 
 class KernelStat(C.Structure):
@@ -454,15 +454,28 @@ class DeviceModel:
         embed_tokens(self.ctx, self.token_embd.scales, self.token_embd.quants, tokens, self.cfg.embd,
                      self.cfg.vocab, self.scratch_bufs["x"])
 
+    def _unfused_scratch(self):
+        """f16 gate, up and down buffers the unfused validation mode writes."""
+        if "ffn_gate" not in self.scratch_bufs:
+            c, sb = self.cfg, self.scratch_bufs
+            for name, w in (("ffn_gate", c.ffn), ("ffn_up", c.ffn), ("ffn_down", c.embd)):
+                sb[name] = HipBuffer.device_only(self.ctx, self.max_n * w * 2)
+            self.scratch.ffn_gate = sb["ffn_gate"].handle
+            self.scratch.ffn_up = sb["ffn_up"].handle
+            self.scratch.ffn_down = sb["ffn_down"].handle
+
     def execute_prefill_ubatch(self, start_pos: int, n: int, logits_all: HipBuffer | None = None,
-                               argmax_all: HipBuffer | None = None):
-        """execute_prefill_ubatch (prefill.rs:337-566)."""
-        if logits_all is None and argmax_all is None:
+                               argmax_all: HipBuffer | None = None, unfused: bool = False):
+        """execute_prefill_ubatch (prefill.rs:337-566). unfused runs every op as its own
+        kernel (validation of the fused GEMM epilogues)."""
+        if unfused:
+            self._unfused_scratch()
+        if logits_all is None and argmax_all is None and not unfused:
             _check(lib().sulimo_hip_execute_prefill_ubatch(self.ctx.handle, C.byref(self.cfg_c),
                                                            C.byref(self.tensors), C.byref(self.kv),
                                                            C.byref(self.scratch), start_pos, n))
         else:
-            o = PrefillOutputsC(_h(logits_all), _h(argmax_all))
+            o = PrefillOutputsC(_h(logits_all), _h(argmax_all), 1 if unfused else 0)
             _check(lib().sulimo_hip_execute_prefill_ubatch_ex(self.ctx.handle, C.byref(self.cfg_c),
                                                               C.byref(self.tensors), C.byref(self.kv),
                                                               C.byref(self.scratch), start_pos, n, C.byref(o)))

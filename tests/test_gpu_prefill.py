@@ -13,31 +13,12 @@ import pytest
 import oracle
 from sulimo_amd import hip
 from sulimo_amd import synthetic as S
-from tests.helpers import cosine
+from tests.helpers import cosine, kv_within_one_step
 
 pytestmark = pytest.mark.gpu
 
 TINY_NEOX = S.ModelConfig(2, 256, 512, 4, 2, 64, 64, 512, 10000.0, 1e-6, 1)
 TINY_NORM = S.ModelConfig(2, 256, 512, 6, 2, 128, 128, 512, 500000.0, 1e-5, 0)
-
-
-def kv_within_one_step(dev_ring, ref_ring, slots, bpp):
-    """test_prefill.rs:829-860 with an explicit error model. The device's K/V inputs differ
-    from the oracle's by the GEMM's rounding (f16 weights), so block scales may differ by a
-    few f16 ulps and codes by one step: codes within +-1, scales within 0.4 %, and every
-    dequantized value within one step plus the scale mismatch on the largest code."""
-    g = dev_ring.reshape(-1, bpp)[slots].reshape(-1, 34)
-    r = ref_ring.reshape(-1, bpp)[slots].reshape(-1, 34)
-    dg = g[:, :2].copy().view(np.float16).astype(np.float32)
-    dr = r[:, :2].copy().view(np.float16).astype(np.float32)
-    cg = g[:, 2:].view(np.int8).astype(np.int32)
-    cr = r[:, 2:].view(np.int8).astype(np.int32)
-    if np.abs(cg - cr).max() > 1:
-        return False
-    if np.any(np.abs(dg - dr) > 4e-3 * np.maximum(dr, 1e-30)):
-        return False
-    bound = 1.05 * np.maximum(dg, dr) + 127.0 * np.abs(dg - dr) + 1e-4
-    return bool(np.all(np.abs(cg * dg - cr * dr) <= bound))
 
 
 def run_both(cfg, seed, chunks, cap, all_logits=False, **model_kw):

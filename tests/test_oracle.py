@@ -236,6 +236,95 @@ def test_embedding_lookup_f16():
         assert np.array_equal(e.view(np.uint16), want.view(np.uint16))
 
 
+def _f16_ulp(v):
+    """Spacing of the f16 grid at |v| (subnormal spacing 2^-24 near zero)."""
+    return np.spacing(np.abs(np.asarray(v, np.float64)).astype(np.float16)).astype(np.float64)
+
+
+def test_cl_rmsnorm_f16_f32w_vs_float64():
+    """rmsnorm_f16_f32w (prefill.cl:4-29) against a float64 RMSNorm rounded once to f16:
+    within one f16 ulp per element, each row normalised by its own mean square, the
+    f32 weight indexed by column, eps inside the square root."""
+    rng = np.random.default_rng(40)
+    n, d, eps = 5, 384, 1e-6
+    x = (rng.standard_normal((n, d)) * np.array([0.1, 1, 3, 20, 0.01])[:, None]).astype(np.float16)
+    w = (1 + rng.normal(0, 0.3, d)).astype(np.float32)
+    out = oracle.cl_rmsnorm_f16_f32w(x, w, d, eps, n).astype(np.float64)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt(np.mean(x64 * x64, axis=1, keepdims=True) + eps) * w
+    assert np.all(np.abs(out - ref) <= _f16_ulp(ref))
+    # eps placement: a row of tiny values, where mean(x^2) = 1e-8 << eps = 1e-6.
+    # 1/sqrt(mean + eps) = 990.1; 1/(sqrt(mean) + eps) would give 9901.
+    tiny = np.full((1, 64), 1e-4, np.float16)
+    o = oracle.cl_rmsnorm_f16_f32w(tiny, np.ones(64, np.float32), 64, 1e-6, 1).astype(np.float64)
+    t64 = float(np.float16(1e-4))
+    want = t64 / np.sqrt(t64 * t64 + 1e-6)
+    assert np.all(np.abs(o - want) <= _f16_ulp(want))
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_cl_rope_f16_vs_complex_rotation(mode):
+    """rope_f16 (prefill.cl:32-68) as the complex rotation (x_a + i x_b) e^{i pos theta_j}
+    with pos = start_pos + token (the head index plays no part), Norm pairs (2j, 2j+1),
+    NeoX pairs (j, j + rope_dim/2), dims past rope_dim untouched, f16 result within one
+    f16 ulp plus the f32 angle's error (pos * 2^-22 relative)."""
+    rng = np.random.default_rng(41 + mode)
+    n, heads, hd, rd, base, start = 4, 3, 64, 48, 1e4, 1021
+    v = rng.standard_normal((n, heads, hd)).astype(np.float16)
+    out = oracle.cl_rope_f16(v, heads, hd, rd, base, mode, start, n).reshape(n, heads, hd).astype(np.float64)
+    j = np.arange(rd // 2)
+    a, b = (2 * j, 2 * j + 1) if mode == 0 else (j, j + rd // 2)
+    v64 = v.astype(np.float64)
+    for t in range(n):
+        pos = start + t
+        th = pos * np.power(float(base), -2.0 * j / rd)
+        z = (v64[t][:, a] + 1j * v64[t][:, b]) * np.exp(1j * th)[None]
+        mag = np.abs(v64[t][:, a]) + np.abs(v64[t][:, b])
+        slack = mag * pos * 2.0 ** -22 + 1e-7
+        assert np.all(np.abs(out[t][:, a] - z.real) <= _f16_ulp(z.real) + slack)
+        assert np.all(np.abs(out[t][:, b] - z.imag) <= _f16_ulp(z.imag) + slack)
+    assert np.array_equal(out[:, :, rd:], v64[:, :, rd:])
+    # position 0 is the identity (cos 0 = 1, sin 0 = 0 exactly)
+    ident = oracle.cl_rope_f16(v[:1], heads, hd, rd, base, mode, 0, 1)
+    assert np.array_equal(ident.view(np.uint16), v[:1].view(np.uint16))
+
+
+def test_cl_silu_mul_f16_vs_float64():
+    """silu_mul_f16 (prefill.cl:240-253): f16(g / (1 + e^-g) * u) within one f16 ulp of
+    the float64 value, gate and up not swapped, large |g| included (e^-g overflows to
+    inf for g <= -89, giving -0 * u)."""
+    rng = np.random.default_rng(43)
+    g = np.concatenate([rng.standard_normal(4000) * 4, [-100.0, -30.0, 0.0, 30.0, 100.0, 60000.0, -60000.0]])
+    u = np.concatenate([rng.standard_normal(4000) * 2, [1.0, 3.0, 7.0, -2.0, 0.5, 1.0, 1.0]])
+    g16, u16 = g.astype(np.float16), u.astype(np.float16)
+    out = oracle.cl_silu_mul_f16(g16, u16).astype(np.float64)
+    g64, u64 = g16.astype(np.float64), u16.astype(np.float64)
+    with np.errstate(over="ignore"):
+        ref = g64 / (1 + np.exp(-g64)) * u64
+    fin = np.abs(ref) <= 65504
+    assert np.all(np.abs(out[fin] - ref[fin]) <= _f16_ulp(ref[fin]))
+    assert np.all(np.isinf(out[~fin]) & (np.sign(out[~fin]) == np.sign(ref[~fin])))
+    assert out[4000] == 0.0 and out[4002] == 0.0
+
+
+def test_cl_add_f16_bit_exact():
+    """add_f16 (prefill.cl:256-266): a = f16(a + b), bit-exact against numpy's binary16
+    addition and against the exact float64 sum rounded once (RNE), including
+    subnormals, cancellation and overflow to inf."""
+    rng = np.random.default_rng(44)
+    a = (rng.standard_normal(20000) * np.exp(rng.uniform(-12, 10, 20000))).astype(np.float16)
+    b = (rng.standard_normal(20000) * np.exp(rng.uniform(-12, 10, 20000))).astype(np.float16)
+    edge_a = np.array([65504, -65504, 6e-8, 1.0, 1.0, 2048, 0.1], np.float16)
+    edge_b = np.array([65504, 32, 6e-8, -1.0, 2.0 ** -11, 1.0, -0.1], np.float16)
+    a, b = np.concatenate([a, edge_a]), np.concatenate([b, edge_b])
+    out = oracle.cl_add_f16(a, b)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(out.view(np.uint16), (a + b).view(np.uint16))
+        exact = (a.astype(np.float64) + b.astype(np.float64)).astype(np.float16)
+    assert np.array_equal(out.view(np.uint16), exact.view(np.uint16))
+    assert np.isinf(out[20000]) and out[20003] == 0.0 and out[20005] == 2048.0
+
+
 def test_kv_store_cl_matches_quantize():
     """prefill.cl:72-116 restated == quantize_f32_to_q8_0 on the f16 values, ring slots
     (start_pos + t) % capacity (test_prefill.rs:56-192 pattern)."""
@@ -335,6 +424,20 @@ def test_forward_token_vs_prefill_reference(extras):
     cos = (lg * lt).sum(1) / np.linalg.norm(lg, axis=1) / np.linalg.norm(lt, axis=1)
     assert cos.min() >= 0.99
     assert np.argmax(lg[-1]) == np.argmax(lt[-1])
+
+
+def test_forward_token_threads_bit_identical():
+    """Splitting forward_token's matvec rows over threads (thread_pool.rs:98-126) leaves
+    every logit and every K/V byte unchanged: each row is one independent dot."""
+    cfg = S.ModelConfig(2, 128, 256, 4, 2, 32, 32, 300, 10000.0, 1e-6, 1)
+    hm = S.make_model(cfg, 2)
+    om = oracle.OracleModel(hm)
+    kv1, kv4 = oracle.OracleKv(cfg, 16), oracle.OracleKv(cfg, 16)
+    for p, t in enumerate(S.random_tokens(3, 6, cfg.vocab)):
+        a = oracle.forward_token(om, kv1, int(t), p)
+        b = oracle.forward_token(om, kv4, int(t), p, threads=4)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert all(np.array_equal(x, y) for x, y in zip(kv1.k + kv1.v, kv4.k + kv4.v))
 
 
 def test_prefill_reference_chunked_equals_whole():
