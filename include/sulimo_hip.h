@@ -136,6 +136,20 @@ int32_t sulimo_hip_enqueue_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_b
                                          const sulimo_hip_buffer *quants,
                                          const sulimo_hip_buffer *x, sulimo_hip_buffer *out,
                                          size_t m, size_t k, size_t n);
+/* No counterpart in the reference: sulimo_hip_enqueue_gemm_q4_0_f16 for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, preconditions and result; it
+ * calls no hipMalloc/hipFree and does not build or use the cached GEMM-layout copy of
+ * the weights. Instead it rebuilds that layout, and keeps its K-split partial sums,
+ * in a static device array of 64 MiB that every GPU the library runs on holds until
+ * the process ends. Matrices whose layout exceeds it (m * k * 18/32 bytes, rounded up
+ * to 32 rows and 64 columns) are rejected with SULIMO_HIP_ERR_INVALID_ARGUMENT. All
+ * calls on one GPU share that array: calls that overlap on one GPU (two contexts'
+ * streams running at once) race and must not be issued. */
+int32_t sulimo_hip_enqueue_gemm_q4_0_f16_noalloc(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
+                                                 const sulimo_hip_buffer *quants,
+                                                 const sulimo_hip_buffer *x, sulimo_hip_buffer *out,
+                                                 size_t m, size_t k, size_t n);
 /* enqueue_rmsnorm (prefill.rs:108-135), prefill.cl:4-29: x f16 [n][d], w f32 [d]. */
 int32_t sulimo_hip_enqueue_rmsnorm(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *x,
                                    const sulimo_hip_buffer *w, sulimo_hip_buffer *out, size_t d,

@@ -44,6 +44,9 @@ struct sulimo_hip_ctx {
   hipEvent_t near_event = nullptr;
   ParkSlot park;
   uint64_t park_want = 0;
+  // This device's copy of the library's static scratch array (no-alloc entry point),
+  // resolved with hipGetSymbolAddress when the context is created.
+  void *scratch = nullptr;
   hipEvent_t t0 = nullptr, t1 = nullptr;
   sulimo_hip_device_info info{};
   // Prefill workspace (grown on demand): f32 residual stream, Q8_0 K/V staging
@@ -190,6 +193,10 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done = nul
 // Partial-sum workspace launch_gemm_q4_0 would use for this GEMM given unlimited room.
 size_t gemm_q4_0_workspace_bytes(const GemmArgs &a);
 
+// Size of the static device scratch array of the no-alloc GEMM entry point (one per
+// device, held until the process ends).
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+
 // Blocks the calling thread until all work queued on ctx->stream is done, without
 // spinning while the GPU runs: the thread sleeps until a host function enqueued after
 // `gate` (an event already recorded on ctx->stream; null = the end of the queue)
@@ -222,6 +229,10 @@ int32_t get_q4_panels(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales, cons
                       const sulimo_hip_buffer *up_scales, const sulimo_hip_buffer *up_quants, int n, int k,
                       const uint8_t **out);
 size_t q4_panel_bytes(int n, int k, bool interleave);
+// Writes the panel copy of (scales, quants) (interleaved with (up_scales, up_quants)
+// when given) to dst, q4_panel_bytes(n, k, up_scales != nullptr) bytes, on stream s.
+int32_t launch_pack_q4_panels(const uint16_t *scales, const uint8_t *quants, const uint16_t *up_scales,
+                              const uint8_t *up_quants, int n, int k, uint8_t *dst, hipStream_t s);
 void release_q4_panels(sulimo_hip_buffer *b);
 // Marks a buffer as written (invalidates panel copies built from it).
 inline void wrote(const sulimo_hip_buffer *b) {

@@ -134,6 +134,48 @@ int32_t sulimo_hip_enqueue_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_b
   return gemm_plain(ctx, scales, quants, x->dev, out->dev, m, k, n, EPI_F16, true);
 }
 
+int32_t sulimo_hip_enqueue_gemm_q4_0_f16_noalloc(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
+                                                 const sulimo_hip_buffer *quants,
+                                                 const sulimo_hip_buffer *x, sulimo_hip_buffer *out,
+                                                 size_t m, size_t k, size_t n) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (k == 0 || k % 32 != 0) return fail(kInval, "K must be a multiple of 32 (Q4_0 block size)");
+  if (m == 0 || m % 8 != 0) return fail(kInval, "M must be a multiple of 8");
+  if (!fits_int(m) || !fits_int(k) || !fits_int(n)) return fail(kInval, "GEMM dimension too large");
+  NEED(scales, m * (k / 32) * 2, "scales");
+  NEED(quants, m * (k / 32) * 16, "quants");
+  NEED(x, n * k * 2, "x");
+  NEED(out, n * m * 2, "out");
+  if (!ctx->scratch) return fail(SULIMO_HIP_ERR_DRIVER, "the device scratch array was not resolved");
+  // The weights' GEMM layout goes to the start of the scratch array (rebuilt on every
+  // call: nothing in the array is assumed to survive from an earlier call), the K-split
+  // partial sums after it. Every byte either region is read from is written first in
+  // the same call, so nothing needs clearing.
+  const size_t pan = q4_panel_bytes((int)m, (int)k, false);
+  const size_t pan_al = (pan + 255) & ~(size_t)255;
+  if (pan_al > kNoAllocScratchBytes)
+    return fail(kInval, "the no-alloc GEMM holds at most " + std::to_string(kNoAllocScratchBytes) +
+                            " bytes of weights in its GEMM layout; this matrix needs " + std::to_string(pan));
+  if (n == 0) return SULIMO_HIP_OK;
+  wrote(out);
+  uint8_t *scr = reinterpret_cast<uint8_t *>(ctx->scratch);
+  if ((rc = launch_pack_q4_panels(dp<const uint16_t>(scales), dp<const uint8_t>(quants), nullptr, nullptr, (int)m,
+                                  (int)k, scr, ctx->stream)))
+    return rc;
+  GemmArgs a{};
+  a.x = dp<const uint16_t>(x);
+  a.m = (int)n;
+  a.k = (int)k;
+  a.ldx = (int)k;
+  a.epi = EPI_F16;
+  a.seg[0] = GemmSegment{scr, out->dev, (int)m, (int)m, 0};
+  a.nseg = 1;
+  a.part = reinterpret_cast<float *>(scr + pan_al);
+  a.part_bytes = kNoAllocScratchBytes - pan_al;
+  return launch_gemm_q4_0(a, ctx->stream);
+}
+
 int32_t sulimo_hip_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
                                  const sulimo_hip_buffer *quants, const sulimo_hip_buffer *x,
                                  sulimo_hip_buffer *out, size_t m, size_t k, size_t n,

@@ -80,6 +80,27 @@ std::mutex g_panel_mu;
 
 }  // namespace
 
+int32_t launch_pack_q4_panels(const uint16_t *scales, const uint8_t *quants, const uint16_t *up_scales,
+                              const uint8_t *up_quants, int n, int k, uint8_t *dst, hipStream_t s) {
+  const bool inter = up_scales != nullptr;
+  PackArgs pa{};
+  pa.scales[0] = scales;
+  pa.quants[0] = quants;
+  pa.scales[1] = inter ? up_scales : scales;
+  pa.quants[1] = inter ? up_quants : quants;
+  pa.out = dst;
+  pa.n = n;
+  pa.nb = k / 32;
+  pa.nst = (pa.nb + 1) / 2;
+  pa.npanels = (n + 31) / 32 * (inter ? 2 : 1);
+  pa.interleave = inter ? 1 : 0;
+  const long total = (long)pa.npanels * pa.nst * kChunks;
+  hipLaunchKernelGGL(pack_q4_panels_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, pa);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return hip_fail(err, "pack_q4_panels_kernel launch");
+  return SULIMO_HIP_OK;
+}
+
 size_t q4_panel_bytes(int n, int k, bool interleave) {
   const size_t np = (size_t)(n + 31) / 32 * (interleave ? 2 : 1);
   const size_t nst = ((size_t)k / 32 + 1) / 2;
@@ -122,23 +143,14 @@ int32_t get_q4_panels(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales, cons
     e.ids[i] = ids[i];
     e.vers[i] = vers[i];
   }
-  PackArgs pa{};
-  pa.scales[0] = reinterpret_cast<const uint16_t *>(scales->dev);
-  pa.quants[0] = reinterpret_cast<const uint8_t *>(quants->dev);
-  pa.scales[1] = inter ? reinterpret_cast<const uint16_t *>(up_scales->dev) : pa.scales[0];
-  pa.quants[1] = inter ? reinterpret_cast<const uint8_t *>(up_quants->dev) : pa.quants[0];
-  pa.out = reinterpret_cast<uint8_t *>(e.dev);
-  pa.n = n;
-  pa.nb = k / 32;
-  pa.nst = (pa.nb + 1) / 2;
-  pa.npanels = (n + 31) / 32 * (inter ? 2 : 1);
-  pa.interleave = inter ? 1 : 0;
-  const long total = (long)pa.npanels * pa.nst * kChunks;
-  hipLaunchKernelGGL(pack_q4_panels_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream, pa);
-  const hipError_t err = hipGetLastError();
-  if (err != hipSuccess) {
+  const int32_t rc = launch_pack_q4_panels(
+      reinterpret_cast<const uint16_t *>(scales->dev), reinterpret_cast<const uint8_t *>(quants->dev),
+      inter ? reinterpret_cast<const uint16_t *>(up_scales->dev) : nullptr,
+      inter ? reinterpret_cast<const uint8_t *>(up_quants->dev) : nullptr, n, k,
+      reinterpret_cast<uint8_t *>(e.dev), ctx->stream);
+  if (rc) {
     hipFree(e.dev);
-    return hip_fail(err, "pack_q4_panels_kernel launch");
+    return rc;
   }
   owner->panels.push_back(e);
   *out = reinterpret_cast<const uint8_t *>(e.dev);

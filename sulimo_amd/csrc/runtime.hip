@@ -101,6 +101,27 @@ static int32_t fill_info(int device, sulimo_hip_device_info *info) {
   return SULIMO_HIP_OK;
 }
 
+// Scratch of sulimo_hip_enqueue_gemm_q4_0_f16_noalloc: the packed weight panels and
+// the K-split partial sums of one GEMM. Each device holds its own copy of this array;
+// host code must use the address hipGetSymbolAddress returns for the device (the
+// array's name on the host is not a device address).
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// Per-device address of `scratch`, resolved once per device with that device current.
+static int32_t resolve_scratch(int device, void **out) {
+  static std::mutex mu;
+  static void *ptrs[64] = {nullptr};
+  std::lock_guard<std::mutex> g(mu);
+  if (!ptrs[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "scratch symbol address");
+    ptrs[device] = p;
+  }
+  *out = ptrs[device];
+  return SULIMO_HIP_OK;
+}
+
 static int32_t create_ctx(int device, bool shared, sulimo_hip_ctx **out) {
   int count = 0;
   hipError_t e = hipGetDeviceCount(&count);
@@ -129,6 +150,16 @@ static int32_t create_ctx(int device, bool shared, sulimo_hip_ctx **out) {
     int32_t r = hip_fail(e, "context creation");
     delete c;
     return r;
+  }
+  if ((rc = resolve_scratch(device, &c->scratch))) {  // device `device` is current here
+    hipEventDestroy(c->done_event);
+    hipEventDestroy(c->near_event);
+    hipEventDestroy(c->t0);
+    hipEventDestroy(c->t1);
+    hipStreamDestroy(c->stream);
+    hipStreamDestroy(c->side);
+    delete c;
+    return rc;
   }
   *out = c;
   return SULIMO_HIP_OK;

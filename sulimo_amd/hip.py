@@ -156,6 +156,7 @@ def _declare(L):
         "sulimo_hip_buffer_map_read": (I32, [P, P, C.POINTER(P)]),
         "sulimo_hip_buffer_unmap": (I32, [P, P, P]),
         "sulimo_hip_enqueue_gemm_q4_0_f16": (I32, [P, P, P, P, P, SZ, SZ, SZ]),
+        "sulimo_hip_enqueue_gemm_q4_0_f16_noalloc": (I32, [P, P, P, P, P, SZ, SZ, SZ]),
         "sulimo_hip_enqueue_rmsnorm": (I32, [P, P, P, P, SZ, F, SZ]),
         "sulimo_hip_enqueue_rope": (I32, [P, P, SZ, SZ, SZ, F, I32, SZ, SZ]),
         "sulimo_hip_enqueue_kv_store": (I32, [P, P, P, SZ, SZ, SZ, SZ]),
@@ -324,6 +325,13 @@ def _h(b):
 
 def enqueue_gemm_q4_0_f16(ctx, scales, quants, x, out, m, k, n):
     _check(lib().sulimo_hip_enqueue_gemm_q4_0_f16(ctx.handle, _h(scales), _h(quants), _h(x), _h(out), m, k, n))
+
+
+def enqueue_gemm_q4_0_f16_noalloc(ctx, scales, quants, x, out, m, k, n):
+    """The same GEMM with no device allocation: its scratch is the library's static
+    per-device array (calls that overlap on one GPU race)."""
+    _check(lib().sulimo_hip_enqueue_gemm_q4_0_f16_noalloc(ctx.handle, _h(scales), _h(quants), _h(x), _h(out),
+                                                          m, k, n))
 
 
 def gemm_q4_0_f16(ctx, scales, quants, x, out, m, k, n) -> GemmProfile:
