@@ -15,8 +15,8 @@ stream; extra.ubatch512 is the same prompt in the reference's default micro-batc
 of 512 tokens, and extra.layer_m512_fused the per-layer time of their Q4_0 linears as
 the prefill runs them (QKV with the RoPE + KV-store epilogue, o, gate/up with SwiGLU,
 down with its residual + norm reduction). `roofline` is the Q4_0 GEMM kernel (the
-dominant kernel), with its per-launch GPU time taken from hipEvents recorded around
-every launch over K more identical steps (the event records slow those steps, so
+dominant kernel: the gate/up projection with its SwiGLU epilogue), with its per-launch
+GPU time taken from hipEvents recorded around every launch over K more identical steps (the event records slow those steps, so
 they are kept out of `value`). `cpu_baseline` times the CPU oracle's restatement of the reference
 forward_token (AVX2, one pinned core) on a bounded sample of the same prompt.
 extra.llama3b_4x4096 is the prefill rate of a Llama-3.2-3B-shaped model (28 layers,
@@ -74,15 +74,16 @@ def copy_calibration(mib: int):
     print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
 
 
-def traffic_from_profiles():
-    """HBM bytes per GEMM launch from the committed rocprofv3 --pmc summary, if present."""
+def traffic_from_profiles(key: str):
+    """HBM bytes (read + written) per launch of one kernel from the committed rocprofv3
+    --pmc summary of the same workload, if present."""
     p = os.path.join(ROOT, "profiles", "gemm_q4_0_prefill2048_pmc.json")
     if not os.path.exists(p):
         return None
     try:
         with open(p) as f:
-            return float(json.load(f)["hbm_bytes_per_gemm_launch"])
-    except (OSError, ValueError, KeyError):
+            return float(json.load(f)["hbm_bytes_per_launch"][key])
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
@@ -238,25 +239,35 @@ def main():
     st = ctx.prefill_stats()
     ctx.set_profiling(False)
 
-    g = st.gemm
-    gemm_ms = g.total_ms / max(g.launches, 1)
-    gemm_tf = g.flop / (g.total_ms * 1e-3) / 1e12 if g.total_ms > 0 else 0.0
-    traffic = traffic_from_profiles()
-    roofline = {"kernel": "gemm_q4_kernel (Q4_0 x f16 MFMA GEMM, all launches of a step)",
-                "bound": "mfma", "achieved": round(gemm_tf, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(gemm_tf / PEAK_F16_TFLOPS, 4), "traffic": traffic,
-                "launches_per_step": g.launches // max(a.steps, 1), "avg_launch_us": round(gemm_ms * 1e3, 2),
-                "flop_per_launch": g.flop / max(g.launches, 1),
+    # The dominant kernel: the gate/up GEMM with the SwiGLU epilogue (one launch per layer,
+    # 2*M*(2*ffn)*hidden FLOPs each, the largest share of the step).
+    g = st.gemm_gate_up
+    gu_us = g.total_ms / max(g.launches, 1) * 1e3
+    gu_flop = g.flop / max(g.launches, 1)
+    gu_tf = gu_flop / (gu_us * 1e-6) / 1e12 if gu_us > 0 else 0.0
+    roofline = {"kernel": "gemm_q4_kernel, gate/up projection with the SwiGLU epilogue "
+                          f"(M={min(a.ubatch, T)} tokens, N=2x{cfg.ffn}, K={cfg.embd})",
+                "bound": "mfma", "achieved": round(gu_tf, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(gu_tf / PEAK_F16_TFLOPS, 4), "traffic": traffic_from_profiles("gate_up"),
+                "launches_per_step": int(g.launches // max(a.steps, 1)), "avg_launch_us": round(gu_us, 2),
+                "flop_per_launch": gu_flop,
                 "timing": f"hipEvents around every launch over {a.steps} further identical steps "
                           f"({wall_ev / a.steps * 1e3:.3f} ms/step with the event records)"}
 
     def cls(k):
         return {"ms_per_step": round(k.total_ms / a.steps, 3), "launches_per_step": int(k.launches // a.steps),
                 "tflops": round(k.flop / (k.total_ms * 1e-3) / 1e12, 2) if k.total_ms > 0 and k.flop > 0 else None,
+                "frac_mfma_peak": round(k.flop / (k.total_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4)
+                if k.total_ms > 0 and k.flop > 0 else None,
                 "gbs": round(k.bytes / (k.total_ms * 1e-3) / 1e9, 1) if k.total_ms > 0 else None}
 
-    extra = {"kernel_classes": {"gemm": cls(st.gemm), "attention": cls(st.attention), "norm": cls(st.norm),
-                                "rope_kv": cls(st.rope_kv)},
+    extra = {"kernel_classes": {"gemm": cls(st.gemm), "gemm_qkv": cls(st.gemm_qkv), "gemm_o": cls(st.gemm_o),
+                                "gemm_gate_up": cls(st.gemm_gate_up), "gemm_down": cls(st.gemm_down),
+                                "gemm_lm_head": cls(st.gemm_lm_head), "attention": cls(st.attention),
+                                "norm": cls(st.norm), "rope_kv": cls(st.rope_kv),
+                                "note": "per-launch hipEvent pairs add a gap before every kernel, so the "
+                                        "class times sum to more than an uninstrumented step; split GEMMs "
+                                        "(o, down) include their K-split reduction"},
              "value_with_event_records": round(T * a.steps / wall_ev, 1),
              "prewarm": {"steps": prewarm_steps, "min_seconds": PREWARM_S},
              "device": ctx.device_info.arch_name.decode()}

@@ -337,6 +337,12 @@ typedef struct {
   sulimo_hip_kernel_stat rope_kv;   /* RoPE + Q8_0 KV quantize/write + ring commit */
   sulimo_hip_kernel_stat other;     /* embedding gather, argmax */
   uint64_t prefill_calls;
+  /* The gemm class by projection (each launch counted there and in gemm): */
+  sulimo_hip_kernel_stat gemm_qkv;     /* q/k/v with the RoPE + Q8_0 K/V store epilogue */
+  sulimo_hip_kernel_stat gemm_o;       /* output projection (+ residual, + its K-split reduction) */
+  sulimo_hip_kernel_stat gemm_gate_up; /* gate and up with the SwiGLU epilogue */
+  sulimo_hip_kernel_stat gemm_down;    /* down projection (+ residual, + its K-split reduction) */
+  sulimo_hip_kernel_stat gemm_lm_head; /* last-token logits */
 } sulimo_hip_prefill_stats;
 
 /* Turns per-launch event timing on or off and clears the statistics. */

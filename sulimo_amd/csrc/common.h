@@ -12,7 +12,11 @@
 #include "../../include/sulimo_hip.h"
 
 // Kernel classes of the prefill statistics (sulimo_hip_prefill_stats fields).
-enum ProfClass : int { PROF_GEMM = 0, PROF_ATTN = 1, PROF_NORM = 2, PROF_ROPE_KV = 3, PROF_OTHER = 4 };
+// The GEMM roles are counted in their own statistic and in the gemm class.
+enum ProfClass : int {
+  PROF_GEMM = 0, PROF_ATTN = 1, PROF_NORM = 2, PROF_ROPE_KV = 3, PROF_OTHER = 4,
+  PROF_GEMM_QKV = 5, PROF_GEMM_O = 6, PROF_GEMM_GATE_UP = 7, PROF_GEMM_DOWN = 8, PROF_GEMM_LM_HEAD = 9
+};
 
 struct ProfRecord {
   int cls;
@@ -214,6 +218,15 @@ __device__ __forceinline__ float rot_sub(float a, float b, float c, float d) {
 __device__ __forceinline__ float rot_add(float a, float b, float c, float d) {
 #pragma clang fp contract(off)
   return a * b + c * d;
+}
+
+// silu(g) * u as the reference's silu_mul_f16 computes it in its OpenCL build, which
+// uses -cl-fast-relaxed-math (kernels/prefill.cl:240-253, crates/sulimo-ocl/src/
+// program.rs:23): the hardware exp2 and reciprocal, within a few f32 ulps of
+// g / (1 + e^-g) * u, far below the f16 rounding that follows. Every kernel that
+// applies SwiGLU uses this, so the fused and the separate SwiGLU give identical bits.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
 // Compute units of the current device (cached per device).

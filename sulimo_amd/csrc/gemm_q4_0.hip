@@ -818,10 +818,9 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
           float v[4];
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            // gate and up rounded to f16 first, as their separate GEMM outputs would be,
-            // then silu_mul_f16's arithmetic (prefill.cl:240-253): g / (1 + e^-g) * u
+            // gate and up rounded to f16 first, as their separate GEMM outputs would be
             const float g = (float)(_Float16)acc[i][f][4 * lq + e], u = (float)(_Float16)acc[i][f + FN / 2][4 * lq + e];
-            v[e] = g / (1.0f + expf(-g)) * u;
+            v[e] = silu_mul(g, u);
           }
           const uint2 o = quad_t16(pack_h2(v[0], v[1]), pack_h2(v[2], v[3]), qj);
           const int col = c0 + wave_n * 16 * FN + 32 * f + cq;

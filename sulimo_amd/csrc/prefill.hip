@@ -615,7 +615,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     g.part = gemm_part;
     g.part_bytes = gemm_ws;
     if (fuse_rope) g.rope = GemmRope{rope_tab, cfg->rope_mode, (int)hd, k_dst, v_dst, slot0, wrap, (int)bpp, wt};
-    if ((rc = timed(ctx, PROF_GEMM, gemm_flop(g), gemm_bytes(g), [&] { return launch_gemm_q4_0(g, s); }))) return rc;
+    if ((rc = timed(ctx, PROF_GEMM_QKV, gemm_flop(g), gemm_bytes(g), [&] { return launch_gemm_q4_0(g, s); }))) return rc;
     bool wrote_window = fuse_rope;
     // 3-4. RoPE on q and k, Q8_0 of k and v into the ring (or staging when wrapping)
     if (!fuse_rope && (rc = timed(ctx, PROF_ROPE_KV, 0, 2.0 * n * (qd + 2 * kvd) + 2.0 * n * qd + 2.0 * n * bpp, [&] {
@@ -664,7 +664,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
       if ((rc = launch_gemm_q4_0(go, s)) ||
           (rc = launch_add_f16_to_f32(xres, dp<const uint16_t>(scratch->ffn_down), n * D, s)))
         return rc;
-    } else if ((rc = timed(ctx, PROF_GEMM, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s, &h_ready); })))
+    } else if ((rc = timed(ctx, PROF_GEMM_O, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s, &h_ready); })))
       return rc;
     // 8. FFN RMSNorm
     if (!h_ready && (rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
@@ -697,7 +697,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
           (rc = launch_silu_mul(dp<const uint16_t>(scratch->ffn_gate), dp<const uint16_t>(scratch->ffn_up),
                                 dp<uint16_t>(scratch->ffn_swiglu), n * F, s)))
         return rc;
-    } else if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gu), gemm_bytes(gu), [&] { return launch_gemm_q4_0(gu, s); })))
+    } else if ((rc = timed(ctx, PROF_GEMM_GATE_UP, gemm_flop(gu), gemm_bytes(gu), [&] { return launch_gemm_q4_0(gu, s); })))
       return rc;
     // 11-12. down projection, residual add fused
     GemmArgs gd{};
@@ -726,7 +726,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
       if ((rc = launch_gemm_q4_0(gd, s)) ||
           (rc = launch_add_f16_to_f32(xres, dp<const uint16_t>(scratch->ffn_down), n * D, s)))
         return rc;
-    } else if ((rc = timed(ctx, PROF_GEMM, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s, &h_ready); })))
+    } else if ((rc = timed(ctx, PROF_GEMM_DOWN, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s, &h_ready); })))
       return rc;
   }
   // 13. output RMSNorm of all n rows (h), final residual back to scratch.x as f16
@@ -737,7 +737,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     return rc;
   // 14. logits of the last token
   const char *hlast = reinterpret_cast<const char *>(scratch->h->dev) + (n - 1) * D * 2;
-  if ((rc = timed(ctx, PROF_GEMM, 2.0 * V * D, V * D * 18.0 / 32.0 + 2.0 * D + 4.0 * V, [&] {
+  if ((rc = timed(ctx, PROF_GEMM_LM_HEAD, 2.0 * V * D, V * D * 18.0 / 32.0 + 2.0 * D + 4.0 * V, [&] {
          return gemm_plain(ctx, tensors->output_scales, tensors->output_quants, hlast, scratch->logits->dev, V, D, 1, EPI_F32);
        })))
     return rc;

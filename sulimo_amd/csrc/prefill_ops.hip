@@ -172,8 +172,7 @@ __global__ void silu_mul_kernel(const _Float16 *g, const _Float16 *u, _Float16 *
                                 size_t total) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
-  const float gv = (float)g[i], uv = (float)u[i];
-  out[i] = (_Float16)(gv / (1.0f + expf(-gv)) * uv);
+  out[i] = (_Float16)silu_mul((float)g[i], (float)u[i]);
 }
 
 __global__ void add_f16_kernel(_Float16 *a, const _Float16 *b, size_t total) {

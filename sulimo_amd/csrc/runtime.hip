@@ -67,16 +67,21 @@ void prof_end(sulimo_hip_ctx *ctx, int ev, int cls, double flop, double bytes) {
 }
 
 void prof_collect(sulimo_hip_ctx *ctx) {
-  sulimo_hip_kernel_stat *st[5] = {&ctx->stats.gemm, &ctx->stats.attention, &ctx->stats.norm,
-                                   &ctx->stats.rope_kv, &ctx->stats.other};
+  sulimo_hip_kernel_stat *st[10] = {&ctx->stats.gemm,     &ctx->stats.attention,    &ctx->stats.norm,
+                                    &ctx->stats.rope_kv,  &ctx->stats.other,        &ctx->stats.gemm_qkv,
+                                    &ctx->stats.gemm_o,   &ctx->stats.gemm_gate_up, &ctx->stats.gemm_down,
+                                    &ctx->stats.gemm_lm_head};
   for (const ProfRecord &r : ctx->pending) {
     float ms = 0.0f;
     if (hipEventElapsedTime(&ms, ctx->ev_pool[2 * r.ev], ctx->ev_pool[2 * r.ev + 1]) != hipSuccess) continue;
-    sulimo_hip_kernel_stat *k = st[r.cls];
-    k->launches++;
-    k->total_ms += ms;
-    k->flop += r.flop;
-    k->bytes += r.bytes;
+    for (int c : {r.cls, r.cls >= PROF_GEMM_QKV ? (int)PROF_GEMM : -1}) {
+      if (c < 0) continue;
+      sulimo_hip_kernel_stat *k = st[c];
+      k->launches++;
+      k->total_ms += ms;
+      k->flop += r.flop;
+      k->bytes += r.bytes;
+    }
   }
   ctx->pending.clear();
 }

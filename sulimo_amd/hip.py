@@ -132,7 +132,9 @@ class KernelStat(C.Structure):
 
 class PrefillStats(C.Structure):
     _fields_ = [("gemm", KernelStat), ("attention", KernelStat), ("norm", KernelStat),
-                ("rope_kv", KernelStat), ("other", KernelStat), ("prefill_calls", C.c_uint64)]
+                ("rope_kv", KernelStat), ("other", KernelStat), ("prefill_calls", C.c_uint64),
+                ("gemm_qkv", KernelStat), ("gemm_o", KernelStat), ("gemm_gate_up", KernelStat),
+                ("gemm_down", KernelStat), ("gemm_lm_head", KernelStat)]
 
 
 def _declare(L):
