@@ -96,9 +96,9 @@ struct Window {
 
 Window window_of(const AttnArgs &a) {
   Window w;
-  w.lo = std::max(0L, (long)a.start_pos - a.capacity + 1);
+  w.lo = a.win_pad > 0 ? 0L : std::max(0L, (long)a.start_pos - a.capacity + 1);
   w.len = (int)((long)a.start_pos + a.n - w.lo);
-  w.pad = (w.len + kKT - 1) / kKT * kKT;
+  w.pad = a.win_pad > 0 ? a.win_pad : (w.len + kKT - 1) / kKT * kKT;
   return w;
 }
 
@@ -672,7 +672,13 @@ int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
   };
   const int nblk = w.pad / kWinKeys;
   int32_t rc;
-  if (a.win_new_done) {
+  if (a.win_pad > 0) {
+    // kept window: the earlier positions not yet valid (and, unless the caller wrote
+    // them, the ubatch's own), nothing past the last position
+    const int jn0 = a.start_pos;
+    const int end = a.win_new_done ? (jn0 + kWinKeys - 1) / kWinKeys : (w.len + kWinKeys - 1) / kWinKeys;
+    if ((rc = window_blocks(std::min(a.win_valid, jn0) / kWinKeys, end))) return rc;
+  } else if (a.win_new_done) {
     const int jn0 = (int)(a.start_pos - w.lo);  // window index of the first new position
     const int pre = (jn0 + kWinKeys - 1) / kWinKeys, tail = w.len / kWinKeys;
     if ((rc = window_blocks(0, pre)) || (rc = window_blocks(std::max(pre, tail), nblk))) return rc;
@@ -681,7 +687,7 @@ int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
   }
   hipError_t e;
   const AttnPlan p = plan_attention(a, w);
-  float *part = reinterpret_cast<float *>(reinterpret_cast<char *>(a.window) + window_bytes(a, w));
+  float *part = a.part ? a.part : reinterpret_cast<float *>(reinterpret_cast<char *>(a.window) + window_bytes(a, w));
   const int n_groups = a.n_head_kv * p.n_hgrp;
   if (p.halves == 2)
     hipLaunchKernelGGL((flash_attn_kernel<HD, 2>), dim3(p.pieces * n_groups), dim3(512), 0, s, a, w.lo, w.pad, p.HG,
@@ -704,6 +710,8 @@ AttnWindowLayout attention_window_layout(const AttnArgs &a) {
   const Window w = window_of(a);
   return AttnWindowLayout{w.lo, w.len, w.pad, w.pad + kVPad};
 }
+
+size_t attention_window_bytes(const AttnArgs &a) { return window_bytes(a, window_of(a)); }
 
 size_t attention_workspace_bytes(const AttnArgs &a) {
   if (a.n <= 0 || a.n_head_kv <= 0 || a.n_head % a.n_head_kv != 0 || a.capacity <= 0) return 0;

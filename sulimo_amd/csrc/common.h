@@ -78,6 +78,19 @@ struct Q4Panels {
   uint64_t vers[4] = {0, 0, 0, 0};  // their write versions when the copy was built
 };
 
+// The f16 copy of a layer's K/V ring that the attention reads (its key window), kept
+// on the K ring buffer between prefills of prompts that fit the ring: window index j =
+// position j, K [n_head_kv][pad][head_dim] then V^T [n_head_kv][head_dim][pad + 64].
+// Positions [0, len) hold f16(code * d) of the ring as it was when the K and V ring
+// buffers had write versions k_ver and v_ver (any other write invalidates it).
+struct KvWindowCache {
+  void *dev = nullptr;
+  size_t bytes = 0;
+  int pad = 0, n_head_kv = 0, head_dim = 0;
+  uint64_t v_id = 0, k_ver = 0, v_ver = 0;
+  long len = 0;
+};
+
 struct sulimo_hip_buffer {
   void *dev = nullptr;
   void *host = nullptr;  // host mirror (the reference's arena slice), may be null
@@ -87,6 +100,7 @@ struct sulimo_hip_buffer {
   uint64_t id = 0;       // unique per created buffer
   uint64_t version = 0;  // bumped by every write through this library
   std::vector<Q4Panels> panels;  // owned GEMM-layout copies (this buffer = their quants)
+  KvWindowCache kvwin;           // attention window of the ring (this buffer = its K ring)
 };
 
 namespace sulimo {
@@ -304,6 +318,13 @@ struct AttnArgs {
   // positions [start_pos, start_pos + n) (the RoPE + Q8_0 store does, from the codes it
   // stores); the window pass then covers only the earlier positions and the padding.
   int win_new_done;
+  // Kept window (start_pos + n <= capacity): win_pad > 0 is its fixed padded length,
+  // window index = position, and positions [0, win_valid) already hold their values;
+  // only the rest of the positions before the ubatch are dequantized. The padding past
+  // the last position holds finite values (zeros or older positions), which the causal
+  // mask removes. part is then where the split-key partials go (else after the window).
+  int win_pad, win_valid;
+  float *part;
 };
 // Device bytes of AttnArgs::window for this attention call (depends on the shapes and
 // on the device's compute-unit count).
@@ -318,6 +339,8 @@ struct AttnWindowLayout {
   int len, pad, vst;
 };
 AttnWindowLayout attention_window_layout(const AttnArgs &a);
+// Bytes of the f16 key window of attention call a (with win_pad set: of the kept window).
+size_t attention_window_bytes(const AttnArgs &a);
 // Column of window index j in a V^T row: inside each group of 16 keys, slots 4-7 and
 // 8-11 are swapped (the order in which the attention reads P^T operands).
 __host__ __device__ inline int window_vt_col(int j) {

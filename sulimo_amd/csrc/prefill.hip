@@ -528,6 +528,39 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   hipStream_t s = ctx->stream;
   const int in = (int)n;
 
+  // Kept attention windows (a prompt that fits the ring): one per layer on its K ring
+  // buffer, valid for the positions the last prefill left in it if nothing else wrote
+  // either ring since. Checked before this call marks the rings written.
+  const bool keep_win = start_pos + n <= cap;
+  std::vector<int> win_valid(L, 0);
+  if (keep_win) {
+    AttnArgs wa = probe_at;
+    wa.win_pad = (int)((cap + 63) / 64 * 64);
+    const size_t wbytes = attention_window_bytes(wa);
+    for (size_t l = 0; l < L; l++) {
+      sulimo_hip_buffer *kb = kv->k_buffers[l], *vb = kv->v_buffers[l];
+      KvWindowCache &wc = kb->kvwin;
+      if (!wc.dev || wc.bytes != wbytes || wc.pad != wa.win_pad || wc.n_head_kv != (int)Hkv ||
+          wc.head_dim != (int)hd || wc.v_id != vb->id) {
+        if (wc.dev) {
+          SULIMO_HIP_TRY(hipStreamSynchronize(ctx->stream));
+          hipFree(wc.dev);
+          wc = KvWindowCache{};
+        }
+        SULIMO_HIP_TRY(hipMalloc(&wc.dev, wbytes));
+        // the padding past the last position must hold finite values
+        SULIMO_HIP_TRY(hipMemsetAsync(wc.dev, 0, wbytes, ctx->stream));
+        wc.bytes = wbytes;
+        wc.pad = wa.win_pad;
+        wc.n_head_kv = (int)Hkv;
+        wc.head_dim = (int)hd;
+        wc.v_id = vb->id;
+      } else if (wc.k_ver == kb->version && wc.v_ver == vb->version) {
+        win_valid[l] = (int)std::min<long>(wc.len, (long)start_pos);
+      }
+      wc.len = 0;  // until this call completes
+    }
+  }
   for (sulimo_hip_buffer *b : {scratch->x, scratch->h, scratch->q, scratch->k, scratch->v, scratch->attn_out,
                                scratch->ffn_swiglu, scratch->logits})
     wrote(b);
@@ -588,6 +621,12 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     at.n_head_kv = (int)Hkv;
     at.head_dim = (int)hd;
     at.window = ws + off_w;
+    if (keep_win) {
+      at.win_pad = kv->k_buffers[l]->kvwin.pad;
+      at.win_valid = win_valid[l];
+      at.window = kv->k_buffers[l]->kvwin.dev;
+      at.part = reinterpret_cast<float *>(ws + off_w + attention_window_bytes(probe_at));
+    }
     const AttnWindowLayout wl = attention_window_layout(at);
     RopeWindowTarget wt{};
     wt.k = reinterpret_cast<uint16_t *>(at.window);
@@ -756,6 +795,14 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   }
   // 15. one wait for the whole ubatch (the thread sleeps while the GPU works)
   rc = wait_parked(ctx, ctx->near_event);
+  if (rc == SULIMO_HIP_OK && keep_win) {
+    for (size_t l = 0; l < L; l++) {  // the kept windows now hold positions [0, start_pos + n)
+      KvWindowCache &wc = kv->k_buffers[l]->kvwin;
+      wc.len = (long)(start_pos + n);
+      wc.k_ver = kv->k_buffers[l]->version;
+      wc.v_ver = kv->v_buffers[l]->version;
+    }
+  }
   if (ctx->prof) {
     prof_collect(ctx);
     ctx->stats.prefill_calls++;

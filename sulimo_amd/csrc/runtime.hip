@@ -358,6 +358,7 @@ int32_t sulimo_hip_buffer_release(sulimo_hip_buffer *buf) {
   if (!buf) return SULIMO_HIP_OK;
   hipSetDevice(buf->device);
   release_q4_panels(buf);
+  if (buf->kvwin.dev) hipFree(buf->kvwin.dev);
   // hipFree waits for work that may still use the allocation.
   hipError_t e = hipFree(buf->dev);
   delete buf;

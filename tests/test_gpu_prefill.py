@@ -247,6 +247,40 @@ def test_cpu_decode_after_gpu_prefill():
     dm.release()
 
 
+@pytest.mark.parametrize("cfg", [TINY_NEOX, TINY_NORM], ids=["neox", "norm"])
+def test_kept_window_follows_ring_writes(cfg):
+    """The attention's f16 copy of the ring is kept between prefills of a prompt that fits
+    the ring, and must follow every other write to it: after a first ubatch, the host
+    rewrites positions 0..23 of every layer's ring (as CPU decode of another sequence
+    would) and pushes them with kv_sync_from_host; the next ubatch must attend to the
+    new bytes. A third ubatch after an untouched second one reuses the kept window."""
+    ctx = hip.HipContext.get_or_init(0)
+    hm = S.make_model(cfg, 61)
+    toks = S.random_tokens(62, 64, cfg.vocab)
+    cap = 96
+    dm = hip.DeviceModel(ctx, hm, cap, 24)
+    om = oracle.OracleModel(hm)
+    dm.embed(toks[:24])
+    dm.execute_prefill_ubatch(0, 24)
+    dm.kv_sync_to_host(0, 24)
+    dk, dv = dm.kv_host()
+    rng = np.random.default_rng(63)
+    for l in range(cfg.n_layers):  # other Q8_0 rows: f16 scale + int8 codes
+        for ring in (dk[l], dv[l]):
+            ring[:24 * dm.bpp] = oracle.quantize_f32_to_q8_0(
+                rng.standard_normal(24 * cfg.kv_dim).astype(np.float32) * 2)
+    dm.kv_sync_from_host(0, 24)
+    okv = oracle.OracleKv(cfg, cap, k=[a.copy() for a in dk], v=[a.copy() for a in dv])
+    for pos, m in ((24, 24), (48, 16)):
+        dm.embed(toks[pos:pos + m])
+        dm.execute_prefill_ubatch(pos, m)
+        g = dm.logits()
+        r = oracle.prefill_reference(om, okv, S.embed_host(hm, toks[pos:pos + m]), pos)
+        assert np.max(np.abs(g - r)) <= 1e-2 * float(np.abs(r).max())
+        assert cosine(g, r) >= 0.999
+    dm.release()
+
+
 def test_llama_3b_four_prompts_of_4096():
     """The Llama-3.2-3B-shaped model at its full size (28 layers, hidden 3072, 24/8
     heads, FFN 8192, vocab 128256, Norm RoPE base 5e5) on 4 independent prompts of 4096
