@@ -226,9 +226,10 @@ def main():
     ms_per_step = wall / a.steps * 1e3
     value = T * a.steps / wall
 
-    # Kernel timing: the same K steps again with a hipEvent pair around every launch on
-    # the library's stream (the records add gaps between kernels, so these steps are
-    # slower and are not `value`; the per-launch kernel durations are what they measure).
+    # Kernel timing: the same K steps again with a hipEvent pair per launch on the
+    # library's stream. The GEMM kernels stamp their pair with their own start and end
+    # (hipExtLaunchKernel); the other launches sit between event records, which add gaps
+    # between kernels, so these steps are slower and are not `value`.
     ctx.set_profiling(True)
     ctx.wait()
     t1 = time.perf_counter()
@@ -251,8 +252,9 @@ def main():
                 "frac": round(gu_tf / PEAK_F16_TFLOPS, 4), "traffic": traffic_from_profiles("gate_up"),
                 "launches_per_step": int(g.launches // max(a.steps, 1)), "avg_launch_us": round(gu_us, 2),
                 "flop_per_launch": gu_flop,
-                "timing": f"hipEvents around every launch over {a.steps} further identical steps "
-                          f"({wall_ev / a.steps * 1e3:.3f} ms/step with the event records)"}
+                "timing": f"hipEvent pair stamped by every gate/up kernel (hipExtLaunchKernel) over "
+                          f"{a.steps} further identical steps ({wall_ev / a.steps * 1e3:.3f} ms/step "
+                          f"with the per-launch events)"}
 
     def cls(k):
         return {"ms_per_step": round(k.total_ms / a.steps, 3), "launches_per_step": int(k.launches // a.steps),
@@ -265,9 +267,10 @@ def main():
                                 "gemm_gate_up": cls(st.gemm_gate_up), "gemm_down": cls(st.gemm_down),
                                 "gemm_lm_head": cls(st.gemm_lm_head), "attention": cls(st.attention),
                                 "norm": cls(st.norm), "rope_kv": cls(st.rope_kv),
-                                "note": "per-launch hipEvent pairs add a gap before every kernel, so the "
-                                        "class times sum to more than an uninstrumented step; split GEMMs "
-                                        "(o, down) include their K-split reduction"},
+                                "note": "GEMM classes: the kernels' own start-to-end times (stamped "
+                                        "events); split GEMMs (o, down) run from the partial-sum kernel's "
+                                        "start to the K-split reduction's end, gap included. Other classes: "
+                                        "event records around the launch, which add a dispatch gap each"},
              "value_with_event_records": round(T * a.steps / wall_ev, 1),
              "prewarm": {"steps": prewarm_steps, "min_seconds": PREWARM_S},
              "device": ctx.device_info.arch_name.decode()}

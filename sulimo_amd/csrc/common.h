@@ -1,6 +1,7 @@
 // common.h - shared declarations of libsulimo_hip.so (host runtime + gfx950 kernels).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -110,11 +111,29 @@ int32_t fail(int32_t code, const std::string &msg);
 int32_t hip_fail(hipError_t e, const char *what);
 // Grows ctx->ws to at least `bytes` (synchronizes the stream before freeing the old one).
 int32_t ensure_workspace(sulimo_hip_ctx *ctx, size_t bytes);
+// Events a launch stamps with its kernels' own start and end times (hipExtLaunchKernel):
+// the interval between them leaves out the dispatch gap that an event recorded on the
+// stream ahead of the launch adds. Both null: an ordinary launch.
+struct LaunchStamp {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
+// Launches kern on s; a non-null start / stop event takes the kernel's start / end time.
+template <typename K, typename... A>
+inline void launch_stamped(K kern, dim3 grid, dim3 block, uint32_t lds, hipStream_t s, hipEvent_t start,
+                           hipEvent_t stop, A... args) {
+  if (start || stop) hipExtLaunchKernelGGL(kern, grid, block, lds, s, start, stop, 0u, args...);
+  else hipLaunchKernelGGL(kern, grid, block, lds, s, args...);
+}
+
 // Event pair around one launch when profiling is on: prof_begin returns the pair
 // index (or -1), prof_end records the end event and queues the record;
 // prof_collect (after the stream drained) adds the elapsed times to ctx->stats.
+// prof_begin_stamp / prof_end_stamp hand the pair to the launch instead (LaunchStamp).
 int prof_begin(sulimo_hip_ctx *ctx);
 void prof_end(sulimo_hip_ctx *ctx, int ev, int cls, double flop, double bytes);
+int prof_begin_stamp(sulimo_hip_ctx *ctx, LaunchStamp *stamp);
+void prof_end_stamp(sulimo_hip_ctx *ctx, int ev, int cls, double flop, double bytes);
 void prof_collect(sulimo_hip_ctx *ctx);
 
 #define SULIMO_HIP_TRY(call)                                   \
@@ -207,7 +226,9 @@ struct GemmArgs {
 // a K split writes f32 partials to a.part (a.part_bytes) and reduces them in a second
 // kernel. With a.norm_w set and norm_done given, *norm_done tells whether that
 // reduction also produced the RMSNorm of the updated rows.
-int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done = nullptr);
+// A non-null stamp takes the start of the first kernel and the end of the last.
+int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done = nullptr,
+                         const LaunchStamp *stamp = nullptr);
 // Partial-sum workspace launch_gemm_q4_0 would use for this GEMM given unlimited room.
 size_t gemm_q4_0_workspace_bytes(const GemmArgs &a);
 

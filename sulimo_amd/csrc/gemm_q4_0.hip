@@ -1101,16 +1101,16 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemmArgs a) {
 }
 
 template <int MT>
-int32_t launch_gemv_mt(const GemmArgs &a, hipStream_t s) {
+int32_t launch_gemv_mt(const GemmArgs &a, hipStream_t s, LaunchStamp st) {
   int panels = 0;
   for (int i = 0; i < a.nseg; i++) panels += (a.seg[i].n + 31) / 32;
   const int kpad = ((a.k / 32 + 1) / 2) * 64;
   const size_t lds = (size_t)MT * kpad * 2;
   const dim3 grid((unsigned)((panels + 3) / 4)), block(256);
   switch (a.epi) {
-    case EPI_F16: hipLaunchKernelGGL((gemv_q4_kernel<MT, EPI_F16>), grid, block, lds, s, a); break;
-    case EPI_F32: hipLaunchKernelGGL((gemv_q4_kernel<MT, EPI_F32>), grid, block, lds, s, a); break;
-    default: hipLaunchKernelGGL((gemv_q4_kernel<MT, EPI_RESID>), grid, block, lds, s, a); break;
+    case EPI_F16: launch_stamped(gemv_q4_kernel<MT, EPI_F16>, grid, block, lds, s, st.start, st.stop, a); break;
+    case EPI_F32: launch_stamped(gemv_q4_kernel<MT, EPI_F32>, grid, block, lds, s, st.start, st.stop, a); break;
+    default: launch_stamped(gemv_q4_kernel<MT, EPI_RESID>, grid, block, lds, s, st.start, st.stop, a); break;
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "gemv_q4_kernel launch");
@@ -1124,10 +1124,10 @@ bool gemv_fits(const GemmArgs &a) {
          (size_t)gemv_tokens(a.m) * kpad * 2 <= (size_t)kGemvMaxXBytes && a.ldx % 8 == 0;
 }
 
-int32_t launch_gemv(const GemmArgs &a, hipStream_t s) {
-  if (a.m == 1) return launch_gemv_mt<1>(a, s);
-  if (a.m == 2) return launch_gemv_mt<2>(a, s);
-  return launch_gemv_mt<4>(a, s);
+int32_t launch_gemv(const GemmArgs &a, hipStream_t s, LaunchStamp st) {
+  if (a.m == 1) return launch_gemv_mt<1>(a, s, st);
+  if (a.m == 2) return launch_gemv_mt<2>(a, s, st);
+  return launch_gemv_mt<4>(a, s, st);
 }
 
 // Splits of nst stages into equal runs with none empty: returns the split count and
@@ -1156,7 +1156,7 @@ int resident_wgs(int threads) {
 }
 
 template <int FM, int FN, int NS = 3, int KSPLIT = 1, int WM = 1>
-int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
+int32_t launch_cfg(const GemmArgs &args, hipStream_t s, LaunchStamp st) {
   constexpr int BM = 32 * FM * WM;
   constexpr int BN = 32 * FN * (4 / WM);
   GemmArgs a = args;
@@ -1177,7 +1177,7 @@ int32_t launch_cfg(const GemmArgs &args, hipStream_t s) {
   const dim3 block(256 * KSPLIT);
   auto go = [&](auto kern, int resident) {
     a.persist = chain && resident >= kXcds && nwork > resident;
-    hipLaunchKernelGGL(kern, dim3(a.persist ? resident : nwork), block, 0, s, a);
+    launch_stamped(kern, dim3(a.persist ? resident : nwork), block, 0, s, st.start, st.stop, a);
   };
   switch (a.epi) {
     case EPI_F16: {
@@ -1359,19 +1359,19 @@ GemmPlan plan_gemm(const GemmArgs &a, bool unbounded) {
   return p;
 }
 
-int32_t launch_plan(const GemmArgs &a, int cfg, hipStream_t s) {
+int32_t launch_plan(const GemmArgs &a, int cfg, hipStream_t s, LaunchStamp st) {
   switch (cfg) {
-    case kT32: return launch_cfg<1, 2, 3, 1>(a, s);
-    case kT32K2: return launch_cfg<1, 2, 3, 2>(a, s);
-    case kT64: return launch_cfg<2, 2, 3, 1>(a, s);
-    case kT64K2: return launch_cfg<2, 2, 3, 2>(a, s);
-    case kT128: return launch_cfg<4, 2, 3, 1>(a, s);
-    case kT128K2: return launch_cfg<4, 2, 3, 2>(a, s);
-    case kN32: return launch_cfg<1, 1, 3, 1>(a, s);
-    case kN32K2: return launch_cfg<1, 1, 3, 2>(a, s);
-    case kN32K4: return launch_cfg<1, 1, 3, 4>(a, s);
-    case kN64: return launch_cfg<2, 1, 3, 1>(a, s);
-    default: return launch_cfg<2, 1, 3, 2>(a, s);
+    case kT32: return launch_cfg<1, 2, 3, 1>(a, s, st);
+    case kT32K2: return launch_cfg<1, 2, 3, 2>(a, s, st);
+    case kT64: return launch_cfg<2, 2, 3, 1>(a, s, st);
+    case kT64K2: return launch_cfg<2, 2, 3, 2>(a, s, st);
+    case kT128: return launch_cfg<4, 2, 3, 1>(a, s, st);
+    case kT128K2: return launch_cfg<4, 2, 3, 2>(a, s, st);
+    case kN32: return launch_cfg<1, 1, 3, 1>(a, s, st);
+    case kN32K2: return launch_cfg<1, 1, 3, 2>(a, s, st);
+    case kN32K4: return launch_cfg<1, 1, 3, 4>(a, s, st);
+    case kN64: return launch_cfg<2, 1, 3, 1>(a, s, st);
+    default: return launch_cfg<2, 1, 3, 2>(a, s, st);
   }
 }
 
@@ -1384,7 +1384,7 @@ size_t gemm_q4_0_workspace_bytes(const GemmArgs &a) {
   return p.splits > 1 ? (size_t)p.splits * a.m * seg_cols(a) * 4 : 0;
 }
 
-int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done) {
+int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done, const LaunchStamp *stamp) {
   if (norm_done) *norm_done = false;
   if (a.m <= 0) return SULIMO_HIP_OK;
   if (a.k <= 0 || a.k % 32 != 0) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "GEMM k must be a positive multiple of 32");
@@ -1419,15 +1419,16 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done) {
     if (r.win.k && (!r.win.vt || r.win.j0 < 0 || r.win.vst % 4 || ((uintptr_t)r.win.vt & 7) || ((uintptr_t)r.win.k & 7)))
       return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "RoPE GEMM window target misaligned");
   }
-  if (gemv_fits(a)) return launch_gemv(a, s);
+  const LaunchStamp st = stamp ? *stamp : LaunchStamp{};
+  if (gemv_fits(a)) return launch_gemv(a, s, st);
   const GemmPlan p = plan_gemm(a, false);
-  if (p.splits == 1) return launch_plan(a, p.cfg, s);
+  if (p.splits == 1) return launch_plan(a, p.cfg, s, st);
   // K split: f32 partials per split, then their sum in split order with the epilogue
   GemmArgs g = a;
   g.epi = EPI_PART;
   g.splits = p.splits;
   g.ldp = seg_cols(a);
-  int32_t rc = launch_plan(g, p.cfg, s);
+  int32_t rc = launch_plan(g, p.cfg, s, LaunchStamp{st.start, nullptr});
   if (rc) return rc;
   GemmArgs r = g;
   r.epi = a.epi;
@@ -1437,11 +1438,11 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done) {
   if (norm_done && a.epi == EPI_RESID && a.norm_w && a.norm_out && a.nseg == 1 && a.seg[0].col0 == 0 && v4 <= 8) {
     const dim3 grid((unsigned)a.m), block(256);
     switch (v4) {
-      case 1: hipLaunchKernelGGL(split_reduce_norm_kernel<1>, grid, block, 0, s, r); break;
-      case 2: hipLaunchKernelGGL(split_reduce_norm_kernel<2>, grid, block, 0, s, r); break;
-      case 3: hipLaunchKernelGGL(split_reduce_norm_kernel<3>, grid, block, 0, s, r); break;
-      case 4: hipLaunchKernelGGL(split_reduce_norm_kernel<4>, grid, block, 0, s, r); break;
-      default: hipLaunchKernelGGL(split_reduce_norm_kernel<8>, grid, block, 0, s, r); break;
+      case 1: launch_stamped(split_reduce_norm_kernel<1>, grid, block, 0, s, nullptr, st.stop, r); break;
+      case 2: launch_stamped(split_reduce_norm_kernel<2>, grid, block, 0, s, nullptr, st.stop, r); break;
+      case 3: launch_stamped(split_reduce_norm_kernel<3>, grid, block, 0, s, nullptr, st.stop, r); break;
+      case 4: launch_stamped(split_reduce_norm_kernel<4>, grid, block, 0, s, nullptr, st.stop, r); break;
+      default: launch_stamped(split_reduce_norm_kernel<8>, grid, block, 0, s, nullptr, st.stop, r); break;
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "split_reduce_norm_kernel launch");
@@ -1451,9 +1452,9 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done) {
   const long threads = (long)a.m * (r.ldp / 4);
   const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
   switch (a.epi) {
-    case EPI_F16: hipLaunchKernelGGL(split_reduce_kernel<EPI_F16>, grid, block, 0, s, r); break;
-    case EPI_F32: hipLaunchKernelGGL(split_reduce_kernel<EPI_F32>, grid, block, 0, s, r); break;
-    default: hipLaunchKernelGGL(split_reduce_kernel<EPI_RESID>, grid, block, 0, s, r); break;
+    case EPI_F16: launch_stamped(split_reduce_kernel<EPI_F16>, grid, block, 0, s, nullptr, st.stop, r); break;
+    case EPI_F32: launch_stamped(split_reduce_kernel<EPI_F32>, grid, block, 0, s, nullptr, st.stop, r); break;
+    default: launch_stamped(split_reduce_kernel<EPI_RESID>, grid, block, 0, s, nullptr, st.stop, r); break;
   }
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? SULIMO_HIP_OK : hip_fail(e, "split_reduce_kernel launch");

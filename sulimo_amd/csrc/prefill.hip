@@ -59,7 +59,7 @@ int32_t begin(sulimo_hip_ctx *ctx) {
 // where no other data lives in it).
 int32_t gemm_plain(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
                    const sulimo_hip_buffer *quants, const void *x, void *out, size_t m, size_t k,
-                   size_t n, int epi, bool own_workspace = false) {
+                   size_t n, int epi, bool own_workspace = false, const LaunchStamp *stamp = nullptr) {
   const uint8_t *pan = nullptr;
   int32_t rc = get_q4_panels(ctx, scales, quants, nullptr, nullptr, (int)m, (int)k, &pan);
   if (rc) return rc;
@@ -79,18 +79,29 @@ int32_t gemm_plain(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
       a.part_bytes = need;
     }
   }
-  return launch_gemm_q4_0(a, ctx->stream);
+  return launch_gemm_q4_0(a, ctx->stream, nullptr, stamp);
 }
 
 // Device pointer of an optional f32 tensor (null when absent).
 const float *opt_f32(const sulimo_hip_buffer *b) { return b ? reinterpret_cast<const float *>(b->dev) : nullptr; }
 
-// Runs one launch between profiling events (no-op events when profiling is off).
+// Runs one launch between profiling events (no events when profiling is off).
 template <typename F>
 int32_t timed(sulimo_hip_ctx *ctx, int cls, double flop, double bytes, F &&launch) {
   const int ev = prof_begin(ctx);
   const int32_t rc = launch();
   prof_end(ctx, ev, cls, flop, bytes);
+  return rc;
+}
+
+// Runs one GEMM (m > 0) whose kernels stamp the profiling events with their own start
+// and end times: launch(stamp), stamp null when profiling is off.
+template <typename F>
+int32_t timed_gemm(sulimo_hip_ctx *ctx, int cls, double flop, double bytes, F &&launch) {
+  LaunchStamp st;
+  const int ev = prof_begin_stamp(ctx, &st);
+  const int32_t rc = launch(ev >= 0 ? &st : nullptr);
+  if (rc == SULIMO_HIP_OK) prof_end_stamp(ctx, ev, cls, flop, bytes);
   return rc;
 }
 
@@ -654,7 +665,9 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     g.part = gemm_part;
     g.part_bytes = gemm_ws;
     if (fuse_rope) g.rope = GemmRope{rope_tab, cfg->rope_mode, (int)hd, k_dst, v_dst, slot0, wrap, (int)bpp, wt};
-    if ((rc = timed(ctx, PROF_GEMM_QKV, gemm_flop(g), gemm_bytes(g), [&] { return launch_gemm_q4_0(g, s); }))) return rc;
+    if ((rc = timed_gemm(ctx, PROF_GEMM_QKV, gemm_flop(g), gemm_bytes(g),
+                         [&](const LaunchStamp *st) { return launch_gemm_q4_0(g, s, nullptr, st); })))
+      return rc;
     bool wrote_window = fuse_rope;
     // 3-4. RoPE on q and k, Q8_0 of k and v into the ring (or staging when wrapping)
     if (!fuse_rope && (rc = timed(ctx, PROF_ROPE_KV, 0, 2.0 * n * (qd + 2 * kvd) + 2.0 * n * qd + 2.0 * n * bpp, [&] {
@@ -703,7 +716,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
       if ((rc = launch_gemm_q4_0(go, s)) ||
           (rc = launch_add_f16_to_f32(xres, dp<const uint16_t>(scratch->ffn_down), n * D, s)))
         return rc;
-    } else if ((rc = timed(ctx, PROF_GEMM_O, gemm_flop(go), gemm_bytes(go), [&] { return launch_gemm_q4_0(go, s, &h_ready); })))
+    } else if ((rc = timed_gemm(ctx, PROF_GEMM_O, gemm_flop(go), gemm_bytes(go),
+                                [&](const LaunchStamp *st) { return launch_gemm_q4_0(go, s, &h_ready, st); })))
       return rc;
     // 8. FFN RMSNorm
     if (!h_ready && (rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D + 4.0 * D, [&] {
@@ -736,7 +750,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
           (rc = launch_silu_mul(dp<const uint16_t>(scratch->ffn_gate), dp<const uint16_t>(scratch->ffn_up),
                                 dp<uint16_t>(scratch->ffn_swiglu), n * F, s)))
         return rc;
-    } else if ((rc = timed(ctx, PROF_GEMM_GATE_UP, gemm_flop(gu), gemm_bytes(gu), [&] { return launch_gemm_q4_0(gu, s); })))
+    } else if ((rc = timed_gemm(ctx, PROF_GEMM_GATE_UP, gemm_flop(gu), gemm_bytes(gu),
+                                [&](const LaunchStamp *st) { return launch_gemm_q4_0(gu, s, nullptr, st); })))
       return rc;
     // 11-12. down projection, residual add fused
     GemmArgs gd{};
@@ -765,7 +780,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
       if ((rc = launch_gemm_q4_0(gd, s)) ||
           (rc = launch_add_f16_to_f32(xres, dp<const uint16_t>(scratch->ffn_down), n * D, s)))
         return rc;
-    } else if ((rc = timed(ctx, PROF_GEMM_DOWN, gemm_flop(gd), gemm_bytes(gd), [&] { return launch_gemm_q4_0(gd, s, &h_ready); })))
+    } else if ((rc = timed_gemm(ctx, PROF_GEMM_DOWN, gemm_flop(gd), gemm_bytes(gd),
+                                [&](const LaunchStamp *st) { return launch_gemm_q4_0(gd, s, &h_ready, st); })))
       return rc;
   }
   // 13. output RMSNorm of all n rows (h), final residual back to scratch.x as f16
@@ -776,9 +792,11 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     return rc;
   // 14. logits of the last token
   const char *hlast = reinterpret_cast<const char *>(scratch->h->dev) + (n - 1) * D * 2;
-  if ((rc = timed(ctx, PROF_GEMM_LM_HEAD, 2.0 * V * D, V * D * 18.0 / 32.0 + 2.0 * D + 4.0 * V, [&] {
-         return gemm_plain(ctx, tensors->output_scales, tensors->output_quants, hlast, scratch->logits->dev, V, D, 1, EPI_F32);
-       })))
+  if ((rc = timed_gemm(ctx, PROF_GEMM_LM_HEAD, 2.0 * V * D, V * D * 18.0 / 32.0 + 2.0 * D + 4.0 * V,
+                       [&](const LaunchStamp *st) {
+                         return gemm_plain(ctx, tensors->output_scales, tensors->output_quants, hlast,
+                                           scratch->logits->dev, V, D, 1, EPI_F32, false, st);
+                       })))
     return rc;
   // Optional per-position logits / top-1.
   if (outputs && (outputs->logits_all || outputs->argmax_all)) {

@@ -66,6 +66,23 @@ void prof_end(sulimo_hip_ctx *ctx, int ev, int cls, double flop, double bytes) {
   ctx->pending.push_back(ProfRecord{cls, ev, flop, bytes});
 }
 
+int prof_begin_stamp(sulimo_hip_ctx *ctx, LaunchStamp *stamp) {
+  if (!ctx->prof) return -1;
+  const int i = (int)ctx->pending.size();
+  while ((int)ctx->ev_pool.size() < 2 * (i + 1)) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return -1;
+    ctx->ev_pool.push_back(e);
+  }
+  stamp->start = ctx->ev_pool[2 * i];
+  stamp->stop = ctx->ev_pool[2 * i + 1];
+  return i;
+}
+
+void prof_end_stamp(sulimo_hip_ctx *ctx, int ev, int cls, double flop, double bytes) {
+  if (ev >= 0) ctx->pending.push_back(ProfRecord{cls, ev, flop, bytes});
+}
+
 void prof_collect(sulimo_hip_ctx *ctx) {
   sulimo_hip_kernel_stat *st[10] = {&ctx->stats.gemm,     &ctx->stats.attention,    &ctx->stats.norm,
                                     &ctx->stats.rope_kv,  &ctx->stats.other,        &ctx->stats.gemm_qkv,
@@ -73,7 +90,10 @@ void prof_collect(sulimo_hip_ctx *ctx) {
                                     &ctx->stats.gemm_lm_head};
   for (const ProfRecord &r : ctx->pending) {
     float ms = 0.0f;
-    if (hipEventElapsedTime(&ms, ctx->ev_pool[2 * r.ev], ctx->ev_pool[2 * r.ev + 1]) != hipSuccess) continue;
+    if (hipEventElapsedTime(&ms, ctx->ev_pool[2 * r.ev], ctx->ev_pool[2 * r.ev + 1]) != hipSuccess) {
+      (void)hipGetLastError();  // not an error of a later launch
+      continue;
+    }
     for (int c : {r.cls, r.cls >= PROF_GEMM_QKV ? (int)PROF_GEMM : -1}) {
       if (c < 0) continue;
       sulimo_hip_kernel_stat *k = st[c];

@@ -175,6 +175,44 @@ def test_split_down_projection_runs_the_next_norm():
     dm.release()
 
 
+def test_profiled_prefill_is_unchanged_and_counts_launches():
+    """Per-launch timing (set_profiling) changes no result: with the GEMM kernels stamping
+    their own start and end events, logits and K/V equal an unprofiled run bit for bit,
+    and the statistics hold one launch of each GEMM role per layer (the down projection
+    splitting K, so its interval runs from the partial-sum kernel to the reduction) plus
+    the LM head, each with a positive time."""
+    cfg = S.ModelConfig(2, 1024, 4096, 8, 2, 128, 128, 512, 1e6, 1e-6, 1)
+    ctx = hip.HipContext.get_or_init(0)
+    hm = S.make_model(cfg, 83, biases=True)
+    toks = S.random_tokens(84, 64, cfg.vocab)
+    dm = hip.DeviceModel(ctx, hm, 128, 64)
+    runs = []
+    try:
+        for prof in (False, True):
+            ctx.set_profiling(prof)
+            dm.embed(toks)
+            dm.execute_prefill_ubatch(0, 64)
+            dm.kv_sync_to_host(0, 64)
+            k, v = dm.kv_host()
+            runs.append((dm.logits(), [a.copy() for a in k], [a.copy() for a in v]))
+        st = ctx.prefill_stats()
+    finally:
+        ctx.set_profiling(False)
+    (l0, k0, v0), (l1, k1, v1) = runs
+    assert np.array_equal(l0, l1)
+    for l in range(cfg.n_layers):
+        assert np.array_equal(k0[l], k1[l]) and np.array_equal(v0[l], v1[l])
+    roles = [st.gemm_qkv, st.gemm_o, st.gemm_gate_up, st.gemm_down]
+    for r in roles:
+        assert r.launches == cfg.n_layers and r.total_ms > 0 and r.flop > 0
+    assert st.gemm_lm_head.launches == 1 and st.gemm_lm_head.total_ms > 0
+    assert st.gemm.launches == 4 * cfg.n_layers + 1
+    total = sum(r.total_ms for r in roles) + st.gemm_lm_head.total_ms
+    assert abs(st.gemm.total_ms - total) <= 1e-6 * total
+    assert st.attention.launches == cfg.n_layers and st.attention.total_ms > 0
+    dm.release()
+
+
 def test_resume_at_1536_with_wrap_at_2048():
     """Edge-shape resume: 1536 positions written in ubatches of 512, then 1024 new tokens
     appended to the capacity-2048 ring, wrapping at 2048 (the last ubatch's queries see
