@@ -187,8 +187,10 @@ __global__ __launch_bounds__(256 * H2, 2 / H2) void flash_attn_kernel(AttnArgs a
   constexpr int K2 = H2 == 2 ? K_BYTES : 16, V2 = H2 == 2 ? V_BYTES : 16;
   __shared__ __attribute__((aligned(16))) char ka0[K_BYTES], va0[V_BYTES], ka1[K_BYTES], va1[V_BYTES];
   __shared__ __attribute__((aligned(16))) char kb0[K2], vb0[V2], kb1[K2], vb1[V2];
-  __shared__ __attribute__((aligned(16))) float comb[H2 == 2 ? 4 * 64 * 16 : 4];  // one O^T tile of the second half
-  __shared__ float cml[H2 == 2 ? 4 * 64 * 2 : 2];                                 // its running max and sum
+  // one O^T tile of the second half, register group g of lane ci at float4 g * 256 + ci
+  // (consecutive lanes, consecutive 16 bytes: no bank conflicts), and its running max and sum
+  __shared__ __attribute__((aligned(16))) float4 comb[H2 == 2 ? 4 * 256 : 1];
+  __shared__ __attribute__((aligned(8))) float2 cml[H2 == 2 ? 256 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = H2 == 2 ? wave >> 2 : 0, qw = wave & 3;
@@ -419,22 +421,19 @@ __global__ __launch_bounds__(256 * H2, 2 / H2) void flash_attn_kernel(AttnArgs a
   // --- the second half hands its (m, l, O^T) to the first, one O^T tile at a time ---
   const int ci = (qw * 64 + lane);
   if constexpr (H2 == 2) {
-  if (half) {
-    cml[2 * ci] = mrun;
-    cml[2 * ci + 1] = lrun;
-  }
+  if (half) cml[ci] = float2{mrun, lrun};
   float a0 = 1.0f, a1 = 0.0f;
 #pragma unroll
   for (int i = 0; i < OT; i++) {
     if (half) {
 #pragma unroll
-      for (int r = 0; r < 16; r += 4)
-        *reinterpret_cast<float4 *>(&comb[ci * 16 + r]) = float4{o[i][r], o[i][r + 1], o[i][r + 2], o[i][r + 3]};
+      for (int g = 0; g < 4; g++) comb[g * 256 + ci] = float4{o[i][4 * g], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3]};
     }
     __syncthreads();
     if (!half) {
       if (i == 0) {
-        const float m1 = cml[2 * ci], l1 = cml[2 * ci + 1];
+        const float2 ml = cml[ci];
+        const float m1 = ml.x, l1 = ml.y;
         const float mm = fmaxf(mrun, m1);
         const float ms = mm == -INFINITY ? 0.0f : mm;
         a0 = __builtin_amdgcn_exp2f(mrun - ms);
@@ -443,7 +442,13 @@ __global__ __launch_bounds__(256 * H2, 2 / H2) void flash_attn_kernel(AttnArgs a
         mrun = mm;  // O and l are now relative to the joint max (a split block's partial keeps it)
       }
 #pragma unroll
-      for (int r = 0; r < 16; r++) o[i][r] = o[i][r] * a0 + comb[ci * 16 + r] * a1;
+      for (int g = 0; g < 4; g++) {
+        const float4 v = comb[g * 256 + ci];
+        o[i][4 * g] = o[i][4 * g] * a0 + v.x * a1;
+        o[i][4 * g + 1] = o[i][4 * g + 1] * a0 + v.y * a1;
+        o[i][4 * g + 2] = o[i][4 * g + 2] * a0 + v.z * a1;
+        o[i][4 * g + 3] = o[i][4 * g + 3] * a0 + v.w * a1;
+      }
     }
     __syncthreads();
   }
