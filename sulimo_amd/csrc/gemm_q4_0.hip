@@ -557,8 +557,10 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     auto slot0 = [&](int part) -> float * {
       return reinterpret_cast<float *>(part == 0 ? smem0 : part == 1 ? smemb0 : part == 2 ? smemc0 : smemd0);
     };
-    const int cidx = (wave * 64 + lane) * RG;
-    float *mine = slot0(kh) + cidx;
+    // registers r .. r+3 of lane cidx at float4 (r / 4) * 256 + cidx: consecutive lanes
+    // write and read consecutive 16 bytes (no bank conflicts)
+    const int cidx = wave * 64 + lane;
+    float4 *mine = reinterpret_cast<float4 *>(slot0(kh)) + cidx;
     lds_barrier();
 #pragma unroll
     for (int i = 0; i < FM; i++)
@@ -569,17 +571,30 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
           if (kh != o) {
 #pragma unroll
             for (int r = 0; r < RG; r += 4)
-              *reinterpret_cast<float4 *>(mine + r) =
+              mine[r / 4 * 256] =
                   float4{acc[i][f][RG * o + r], acc[i][f][RG * o + r + 1], acc[i][f][RG * o + r + 2], acc[i][f][RG * o + r + 3]};
           }
           lds_barrier();
           if (kh == o) {
 #pragma unroll
-            for (int r = 0; r < RG; r++) {
-              float v = o == 0 ? acc[i][f][RG * o + r] : slot0(0)[cidx + r];
+            for (int r = 0; r < RG; r += 4) {
+              float w[KSPLIT][4];
 #pragma unroll
-              for (int p = 1; p < KSPLIT; p++) v += p == o ? acc[i][f][RG * o + r] : slot0(p)[cidx + r];
-              acc[i][f][RG * o + r] = v;
+              for (int p = 0; p < KSPLIT; p++) {
+                if (p == o) continue;
+                const float4 t = reinterpret_cast<const float4 *>(slot0(p))[r / 4 * 256 + cidx];
+                w[p][0] = t.x;
+                w[p][1] = t.y;
+                w[p][2] = t.z;
+                w[p][3] = t.w;
+              }
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                float v = o == 0 ? acc[i][f][RG * o + r + e] : w[0][e];
+#pragma unroll
+                for (int p = 1; p < KSPLIT; p++) v += p == o ? acc[i][f][RG * o + r + e] : w[p][e];
+                acc[i][f][RG * o + r + e] = v;
+              }
             }
           }
           lds_barrier();
