@@ -16,9 +16,13 @@ of 512 tokens, and extra.layer_m512_fused the per-layer time of their Q4_0 linea
 the prefill runs them (QKV with the RoPE + KV-store epilogue, o, gate/up with SwiGLU,
 down with its residual + norm reduction). `roofline` is the Q4_0 GEMM kernel (the
 dominant kernel: the gate/up projection with its SwiGLU epilogue), with its per-launch
-GPU time taken from hipEvents recorded around every launch over K more identical steps (the event records slow those steps, so
-they are kept out of `value`). `cpu_baseline` times the CPU oracle's restatement of the reference
-forward_token (AVX2, one pinned core) on a bounded sample of the same prompt.
+GPU time taken from a hipEvent pair that each of its launches stamps with the kernel's
+own start and end (hipExtLaunchKernelGGL) over K more identical steps (the other
+launches of those steps sit between recorded events, which slow the steps, so they
+are kept out of `value`); `traffic` is its HBM bytes per launch from the committed
+rocprofv3 counter summary. `cpu_baseline` times the CPU oracle's restatement of the
+reference forward_token (AVX2, one pinned core, plus an all-cores extension) on a
+bounded sample of the same prompt.
 extra.llama3b_4x4096 is the prefill rate of a Llama-3.2-3B-shaped model (28 layers,
 hidden 3072, 24/8 heads, FFN 8192, vocab 128256) over 4 independent prompts of 4096
 tokens, each in one ubatch on a ring of 4096 positions.
