@@ -94,6 +94,23 @@ __device__ __forceinline__ void dq4(uint32_t nib, half2v d2, half2v &a, half2v &
   }
 }
 
+// The same four nibbles -> two half2 of q-8 (exact, unscaled).
+template <bool HI>
+__device__ __forceinline__ void dq4_raw(uint32_t nib, half2v &a, half2v &b) {
+  const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, nib, 0x04010400u);
+  const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, nib, 0x04030402u);
+  if constexpr (HI) {
+    const half2v s = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const half2v o = {(_Float16)-72.0f, (_Float16)-72.0f};
+    a = __builtin_elementwise_fma(as_h2(p0), s, o);
+    b = __builtin_elementwise_fma(as_h2(p1), s, o);
+  } else {
+    const half2v o = {(_Float16)1032.0f, (_Float16)1032.0f};
+    a = as_h2(p0) - o;
+    b = as_h2(p1) - o;
+  }
+}
+
 // s_waitcnt vmcnt(n) with expcnt and lgkmcnt left unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -1031,10 +1048,11 @@ __global__ __launch_bounds__(256) void split_reduce_norm_kernel(GemmArgs a) {
 
 // GEMV for MT <= 4 tokens (decode, the last-token LM head): HBM-bound, so no MFMA and
 // no LDS staging of the weights. One wave per 32-row panel reads the panel's records
-// (lane l: quant bytes at 16*l, its row's two scales) U stages at a time, dequantizes
-// with the GEMM's f16 rounding and accumulates f16 x f16 products in f32
-// (v_dot2_f32_f16) against x held in LDS; the two half-waves of a row combine at the
-// end. x beyond K is zero in LDS, so the odd-block half stage adds nothing.
+// (lane l: quant bytes at 16*l, its row's two scales) U stages at a time and, in the
+// order of logits_f16_output (kernels/prefill.cl:269-308), sums each block's x*(q-8)
+// in f32 (exact f16 q-8 products, v_dot2_f32_f16, against x held in LDS) before one
+// multiply by the block's d; the two half-waves of a row combine at the end. x beyond
+// K is zero in LDS, so the odd-block half stage adds nothing.
 constexpr int kGemvMaxXBytes = 64 * 1024;
 
 template <int MT, int EPI>
@@ -1079,22 +1097,25 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(GemmArgs a) {
 #pragma unroll
       for (int b = 0; b < 2; b++) {
         const uint32_t lo = b ? qv[u].z : qv[u].x, hi = b ? qv[u].w : qv[u].y;
-        const half2v d2 = as_h2(__builtin_amdgcn_perm(sw[u], sw[u], b ? 0x03020302u : 0x01000100u));
-        half2v w[8];  // elements 8h .. 8h+7, then 16+8h .. 16+8h+7 of block b
-        dq4<false>(lo & 0x0F0F0F0Fu, d2, w[0], w[1]);
-        dq4<false>(hi & 0x0F0F0F0Fu, d2, w[2], w[3]);
-        dq4<true>(lo & 0xF0F0F0F0u, d2, w[4], w[5]);
-        dq4<true>(hi & 0xF0F0F0F0u, d2, w[6], w[7]);
+        const float d = (float)as_h2(sw[u])[b];
+        half2v w[8];  // q-8 of elements 8h .. 8h+7, then 16+8h .. 16+8h+7 of block b
+        dq4_raw<false>(lo & 0x0F0F0F0Fu, w[0], w[1]);
+        dq4_raw<false>(hi & 0x0F0F0F0Fu, w[2], w[3]);
+        dq4_raw<true>(lo & 0xF0F0F0F0u, w[4], w[5]);
+        dq4_raw<true>(hi & 0xF0F0F0F0u, w[6], w[7]);
+        // the reference's order: the block's sum of x*(q-8), then one multiply by d
 #pragma unroll
         for (int t = 0; t < MT; t++) {
           const _Float16 *xr = xs + t * kpad + kb + 32 * b + 8 * h;
           const half8 xl = *reinterpret_cast<const half8 *>(xr);
           const half8 xh = *reinterpret_cast<const half8 *>(xr + 16);
+          float bs = 0.0f;
 #pragma unroll
           for (int j = 0; j < 4; j++) {
-            acc[t] = __builtin_amdgcn_fdot2(w[j], half2v{xl[2 * j], xl[2 * j + 1]}, acc[t], false);
-            acc[t] = __builtin_amdgcn_fdot2(w[4 + j], half2v{xh[2 * j], xh[2 * j + 1]}, acc[t], false);
+            bs = __builtin_amdgcn_fdot2(w[j], half2v{xl[2 * j], xl[2 * j + 1]}, bs, false);
+            bs = __builtin_amdgcn_fdot2(w[4 + j], half2v{xh[2 * j], xh[2 * j + 1]}, bs, false);
           }
+          acc[t] += bs * d;
         }
       }
     }
