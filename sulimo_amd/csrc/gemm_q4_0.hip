@@ -169,6 +169,10 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   constexpr int NX = FM * WM;                     // X DMA instructions per wave per stage
   constexpr int NQ = FN * WN / 4;                 // quant DMA instructions per wave per stage
   constexpr int NDMA = NX + NQ + 1;               // + one scale DMA per wave per stage
+  // Order of a stage's DMA group. Tiles with at least twice as many X as quant
+  // instructions issue the weights (quants, scales) first: measured 1-2.6 % faster on
+  // those kernels and 0.4-2.2 % slower on the others (same-box kernel traces).
+  constexpr bool kWeightsFirst = NX >= 2 * NQ;
   constexpr int X_BYTES = BM * kBK * 2;
   constexpr int Q_BYTES = BN * 32;
   constexpr int S_BYTES = BN * 4;
@@ -335,14 +339,25 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
     const int sst = st < nst ? st : 0;
     bool half = false;
     if constexpr (decltype(kCheck)::value) half = (2 * sst + 1 == nb);
+    auto x_part = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < NX; i++) {
-      const uint32_t off = (half && xhi[i]) ? kOob : xoff[i];
-      dma16(rx, slot + 8 * (NX * wave + i) * kBK * 2, off, sst * kBK * 2);
+      for (int i = 0; i < NX; i++) {
+        const uint32_t off = (half && xhi[i]) ? kOob : xoff[i];
+        dma16(rx, slot + 8 * (NX * wave + i) * kBK * 2, off, sst * kBK * 2);
+      }
+    };
+    auto w_part = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int f = 0; f < NQ; f++) dma16(rp, slot + X_BYTES + (NQ * wave + f) * 1024, qoff[f], sst * kQ4PanelRecord);
+      if (lane < 8 * NQ) dma16(rp, slot + X_BYTES + Q_BYTES + NQ * wave * 128, soff, sst * kQ4PanelRecord);
+    };
+    if constexpr (kWeightsFirst) {
+      w_part();
+      x_part();
+    } else {
+      x_part();
+      w_part();
     }
-#pragma unroll
-    for (int f = 0; f < NQ; f++) dma16(rp, slot + X_BYTES + (NQ * wave + f) * 1024, qoff[f], sst * kQ4PanelRecord);
-    if (lane < 8 * NQ) dma16(rp, slot + X_BYTES + Q_BYTES + NQ * wave * 128, soff, sst * kQ4PanelRecord);
   };
 
   floatx16 acc[FM][FN];
@@ -375,11 +390,23 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
   uint32_t nxoff[NX], nqoff[NQ], nsoff;
   auto issue_next = [&](auto J, int nsst) __attribute__((always_inline)) {
     char *slot = slot_ptr(ic<0>{}, J);
+    auto x_part = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < NX; i++) dma16(rx, slot + 8 * (NX * wave + i) * kBK * 2, nxoff[i], nsst * kBK * 2);
+      for (int i = 0; i < NX; i++) dma16(rx, slot + 8 * (NX * wave + i) * kBK * 2, nxoff[i], nsst * kBK * 2);
+    };
+    auto w_part = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int f = 0; f < NQ; f++) dma16(rp, slot + X_BYTES + (NQ * wave + f) * 1024, nqoff[f], nsst * kQ4PanelRecord);
-    if (lane < 8 * NQ) dma16(rp, slot + X_BYTES + Q_BYTES + NQ * wave * 128, nsoff, nsst * kQ4PanelRecord);
+      for (int f = 0; f < NQ; f++)
+        dma16(rp, slot + X_BYTES + (NQ * wave + f) * 1024, nqoff[f], nsst * kQ4PanelRecord);
+      if (lane < 8 * NQ) dma16(rp, slot + X_BYTES + Q_BYTES + NQ * wave * 128, nsoff, nsst * kQ4PanelRecord);
+    };
+    if constexpr (kWeightsFirst) {
+      w_part();
+      x_part();
+    } else {
+      x_part();
+      w_part();
+    }
   };
   auto next_offsets = [&]() __attribute__((always_inline)) {
     int ntm, ntn;
