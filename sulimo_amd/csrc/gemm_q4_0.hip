@@ -1005,6 +1005,77 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs a) {
   }
 }
 
+// The same for rows of 256*V columns, one wave per row: lane l holds columns 256j + 4l ..
+// +3 (j < V), the layout and summation order of the RMSNorm kernels (rmsnorm_vec_kernel),
+// so the normed rows equal theirs on the updated residual bit for bit, and the row's sum
+// of squares needs no workgroup barrier.
+template <int V>
+__global__ __launch_bounds__(256) void split_reduce_norm_vec_kernel(GemmArgs a) {
+  typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+  constexpr int D = 256 * V;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= a.m) return;
+  const GemmSegment seg = a.seg[0];
+  const size_t plane = (size_t)a.m * a.ldp;
+  const float *p = a.part + (size_t)row * a.ldp;
+  float *x = reinterpret_cast<float *>(seg.out) + (size_t)row * seg.ldo;
+  // every load before the first store (loads and stores retire in issue order)
+  float4 v[V], nw[V], old[V];
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const int c = 256 * j + 4 * lane;
+    nw[j] = *reinterpret_cast<const float4 *>(a.norm_w + c);
+    v[j] = *reinterpret_cast<const float4 *>(p + c);
+    old[j] = *reinterpret_cast<const float4 *>(x + c);
+  }
+  for (int sp = 1; sp < a.splits; sp++) {
+    float4 w[V];
+#pragma unroll
+    for (int j = 0; j < V; j++) w[j] = *reinterpret_cast<const float4 *>(p + sp * plane + 256 * j + 4 * lane);
+#pragma unroll
+    for (int j = 0; j < V; j++) {
+      v[j].x += w[j].x;
+      v[j].y += w[j].y;
+      v[j].z += w[j].z;
+      v[j].w += w[j].w;
+    }
+  }
+  if (seg.bias) {
+#pragma unroll
+    for (int j = 0; j < V; j++) {
+      const float4 b = *reinterpret_cast<const float4 *>(seg.bias + 256 * j + 4 * lane);
+      v[j].x += b.x;
+      v[j].y += b.y;
+      v[j].z += b.z;
+      v[j].w += b.w;
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const float4 nx = float4{old[j].x + (float)(_Float16)v[j].x, old[j].y + (float)(_Float16)v[j].y,
+                             old[j].z + (float)(_Float16)v[j].z, old[j].w + (float)(_Float16)v[j].w};
+    *reinterpret_cast<float4 *>(x + 256 * j + 4 * lane) = nx;
+    v[j] = nx;
+  }
+#pragma unroll
+  for (int j = 0; j < V; j++) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float scale = 1.0f / sqrtf(ss / (float)D + a.norm_eps);
+  _Float16 *out = reinterpret_cast<_Float16 *>(a.norm_out) + (size_t)row * D;
+#pragma unroll
+  for (int j = 0; j < V; j++) {
+    const int c = 256 * j + 4 * lane;
+    const float4 wv = nw[j];
+    *reinterpret_cast<half4v *>(out + c) = half4v{(_Float16)(v[j].x * scale * wv.x), (_Float16)(v[j].y * scale * wv.y),
+                                                  (_Float16)(v[j].z * scale * wv.z), (_Float16)(v[j].w * scale * wv.w)};
+    if (a.norm_x16)
+      *reinterpret_cast<half4v *>(reinterpret_cast<_Float16 *>(a.norm_x16) + (size_t)row * D + c) =
+          half4v{(_Float16)v[j].x, (_Float16)v[j].y, (_Float16)v[j].z, (_Float16)v[j].w};
+  }
+}
+
 // K-split reduction of an EPI_RESID GEMM fused with the RMSNorm of the rows it updates:
 // one workgroup per row holding its V*1024 columns in registers. x += f16(partials summed
 // in split order (+ bias)), as split_reduce_kernel does, then norm_out = f16(x * scale *
@@ -1499,6 +1570,23 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done, cons
   // the residual update and the RMSNorm of its rows in one pass, rows up to 8192 wide
   const int v4 = (a.seg[0].n / 4 + 255) / 256;
   if (norm_done && a.epi == EPI_RESID && a.norm_w && a.norm_out && a.nseg == 1 && a.seg[0].col0 == 0 && v4 <= 8) {
+    const int n = a.seg[0].n;
+    if (n % 256 == 0 && n <= 256 * 16) {  // one wave per row
+      const dim3 grid((unsigned)((a.m + 3) / 4)), block(256);
+      switch (n / 256) {
+#define SULIMO_SRN_CASE(V) \
+  case V: launch_stamped(split_reduce_norm_vec_kernel<V>, grid, block, 0, s, nullptr, st.stop, r); break;
+        SULIMO_SRN_CASE(1) SULIMO_SRN_CASE(2) SULIMO_SRN_CASE(3) SULIMO_SRN_CASE(4) SULIMO_SRN_CASE(5)
+        SULIMO_SRN_CASE(6) SULIMO_SRN_CASE(7) SULIMO_SRN_CASE(8) SULIMO_SRN_CASE(9) SULIMO_SRN_CASE(10)
+        SULIMO_SRN_CASE(11) SULIMO_SRN_CASE(12) SULIMO_SRN_CASE(13) SULIMO_SRN_CASE(14) SULIMO_SRN_CASE(15)
+        SULIMO_SRN_CASE(16)
+#undef SULIMO_SRN_CASE
+      }
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return hip_fail(e, "split_reduce_norm_vec_kernel launch");
+      *norm_done = true;
+      return SULIMO_HIP_OK;
+    }
     const dim3 grid((unsigned)a.m), block(256);
     switch (v4) {
       case 1: launch_stamped(split_reduce_norm_kernel<1>, grid, block, 0, s, nullptr, st.stop, r); break;
