@@ -320,9 +320,11 @@ int32_t sulimo_hip_kv_sync_from_host(sulimo_hip_ctx *ctx, const sulimo_hip_kv_ca
                                      size_t start_pos, size_t n);
 
 /* ---- timing (the queue's CL_QUEUE_PROFILING_ENABLE, program.rs:145-153) ---- */
-/* Per kernel class GPU time of execute_prefill_ubatch launches, measured with
- * hipEvents recorded around each launch on the context stream while profiling is
- * on, plus the algorithmic work the launches performed. */
+/* Per kernel class GPU time of execute_prefill_ubatch launches while profiling is on,
+ * plus the algorithmic work the launches performed. The GEMM kernels stamp a hipEvent
+ * pair with their own start and end (a K-split GEMM: the partial-sum kernel's start
+ * and the reduction's end); the other launches sit between hipEvents recorded on the
+ * context stream. */
 typedef struct {
   uint64_t launches;
   double total_ms;
