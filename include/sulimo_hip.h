@@ -319,6 +319,26 @@ int32_t sulimo_hip_kv_sync_to_host(sulimo_hip_ctx *ctx, const sulimo_hip_kv_cach
 int32_t sulimo_hip_kv_sync_from_host(sulimo_hip_ctx *ctx, const sulimo_hip_kv_cache *kv,
                                      size_t start_pos, size_t n);
 
+/* Validation accessors (no counterpart in the reference, whose attention reads the
+ * Q8_0 ring directly, kernels/prefill.cl:120-237).
+ *
+ * kv_window_download: the f16 attention window the prefill keeps for `layer` when a
+ * prompt fits the ring (start_pos + n <= capacity; window index = position). Layout
+ * (f16): K [n_head_kv][pad][head_dim], then V transposed, n_head_kv * head_dim rows of
+ * v_row_stride elements; position j of a V^T row sits at column j with slots 4-7 and
+ * 8-11 of each group of 16 swapped. Entries [0, valid_len) equal f16(code * f16(d)) of
+ * the ring; valid_len is 0 once either ring buffer was written outside the prefill.
+ * host == NULL only reports bytes, valid_len, pad and v_row_stride. Blocking.
+ *
+ * rope_table: the cos/sin pairs every RoPE rotation of a ubatch uses, f32
+ * [n][rope_dim/2][2] = (cos, sin) of (start_pos + t) / freq_base^(2i/rope_dim)
+ * (the angle of prefill.cl:32-68). */
+int32_t sulimo_hip_kv_window_download(sulimo_hip_ctx *ctx, const sulimo_hip_kv_cache *kv, int32_t layer,
+                                      void *host, size_t host_bytes, size_t *bytes, int64_t *valid_len,
+                                      int32_t *pad, int32_t *v_row_stride);
+int32_t sulimo_hip_rope_table(sulimo_hip_ctx *ctx, size_t rope_dim, float freq_base, size_t start_pos,
+                              size_t n, sulimo_hip_buffer *table);
+
 /* ---- timing (the queue's CL_QUEUE_PROFILING_ENABLE, program.rs:145-153) ---- */
 /* Per kernel class GPU time of execute_prefill_ubatch launches while profiling is on,
  * plus the algorithmic work the launches performed. The GEMM kernels stamp a hipEvent

@@ -103,7 +103,7 @@ def _declare(L):
         "orc_forward_token": (_I, [C.POINTER(OrcModel), C.POINTER(OrcKv), C.c_uint32, _SZ, _P]),
         "orc_forward_token_mt": (_I, [C.POINTER(OrcModel), C.POINTER(OrcKv), C.c_uint32, _SZ, _P, _I]),
         "orc_prefill_reference": (_I, [C.POINTER(OrcModel), C.POINTER(OrcKv), _P, _SZ, _SZ, _I,
-                                       _P, _P]),
+                                       _P, _P, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -355,16 +355,23 @@ def forward_token(om: OracleModel, kv: OracleKv, token: int, pos: int, threads: 
 
 
 def prefill_reference(om: OracleModel, kv: OracleKv, x_in, start_pos: int, all_logits=False,
-                      want_h=False):
-    """fp32 reference prefill (prefill.rs:362-560 op order, test_prefill.rs rounding)."""
+                      want_h=False, want_x=False):
+    """fp32 reference prefill (prefill.rs:362-560 op order, test_prefill.rs rounding).
+    Returns the logits; with want_h and/or want_x a tuple (logits[, h_final][, x_final]):
+    h_final the f32 output-normed hidden states [n, embd], x_final the f32 residual stream
+    after the last layer [n, embd] (scratch.x and scratch.h of the device prefill)."""
     x_in = _f16(x_in)
     n = x_in.shape[0]
     V = om.cfg.vocab
     logits = np.zeros((n, V) if all_logits else (V,), np.float32)
     h = np.zeros((n, om.cfg.embd), np.float32) if want_h else None
+    xf = np.zeros((n, om.cfg.embd), np.float32) if want_x else None
     rc = lib().orc_prefill_reference(C.byref(om.model), C.byref(kv.s), _p(x_in), start_pos, n,
                                      1 if all_logits else 0, _p(logits),
-                                     _p(h) if h is not None else None)
+                                     _p(h) if h is not None else None,
+                                     _p(xf) if xf is not None else None)
     if rc:
         raise MemoryError("orc_prefill_reference failed")
-    return (logits, h) if want_h else logits
+    if not (want_h or want_x):
+        return logits
+    return (logits,) + ((h,) if want_h else ()) + ((xf,) if want_x else ())

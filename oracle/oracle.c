@@ -612,7 +612,7 @@ static int gemm_f16io(orc_q4 w, const float *x16, size_t m, size_t k, size_t n, 
 }
 
 int orc_prefill_reference(const orc_model *m, orc_kv *kv, const uint16_t *x_in, size_t start_pos,
-                          size_t n, int all_logits, float *logits, float *h_final) {
+                          size_t n, int all_logits, float *logits, float *h_final, float *x_final) {
   const orc_config *c = &m->cfg;
   size_t D = c->embd, F = c->ffn, hd = c->head_dim;
   size_t qd = (size_t)c->n_head * hd, kvd = (size_t)c->n_head_kv * hd;
@@ -720,6 +720,7 @@ int orc_prefill_reference(const orc_model *m, orc_kv *kv, const uint16_t *x_in, 
   if (rc) goto done;
   for (size_t t = 0; t < n; t++) orc_rmsnorm_scalar(x + t * D, m->output_norm, c->eps, D, h + t * D);
   if (h_final) memcpy(h_final, h, n * D * 4);
+  if (x_final) memcpy(x_final, x, n * D * 4);
   if (all_logits)
     rc = gemm_q4_f32x(m->output.scales, m->output.quants, h, c->vocab, D, n, logits, c->vocab);
   else

@@ -158,9 +158,11 @@ int orc_forward_token_mt(const orc_model *m, orc_kv *kv, uint32_t token, size_t 
  * x_in: f16 [n][embd] token embeddings. Attention is a sliding window of the
  * last `capacity` positions; new K/V are committed to the ring after attention.
  * logits: f32 [vocab] of token n-1, or [n][vocab] when all_logits != 0.
- * h_final (optional): f32 [n][embd] output-normed hidden states. */
+ * h_final (optional): f32 [n][embd] output-normed hidden states.
+ * x_final (optional): f32 [n][embd] residual stream after the last layer (the input of
+ * the output norm). */
 int orc_prefill_reference(const orc_model *m, orc_kv *kv, const uint16_t *x_in, size_t start_pos,
-                          size_t n, int all_logits, float *logits, float *h_final);
+                          size_t n, int all_logits, float *logits, float *h_final, float *x_final);
 
 #ifdef __cplusplus
 }

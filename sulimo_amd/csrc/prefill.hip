@@ -413,6 +413,47 @@ int32_t sulimo_hip_kv_sync_from_host(sulimo_hip_ctx *ctx, const sulimo_hip_kv_ca
   return kv_sync(ctx, kv, start_pos, n, false);
 }
 
+int32_t sulimo_hip_kv_window_download(sulimo_hip_ctx *ctx, const sulimo_hip_kv_cache *kv, int32_t layer,
+                                      void *host, size_t host_bytes, size_t *bytes, int64_t *valid_len,
+                                      int32_t *pad, int32_t *v_row_stride) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (!kv || !kv->k_buffers || !kv->v_buffers || layer < 0 || layer >= kv->n_layers)
+    return fail(kInval, "bad kv cache or layer");
+  const sulimo_hip_buffer *kb = kv->k_buffers[layer], *vb = kv->v_buffers[layer];
+  if (!kb || !vb) return fail(kInval, "null kv buffer");
+  const KvWindowCache &wc = kb->kvwin;
+  if (!wc.dev) return fail(kInval, "no kept attention window for this layer");
+  AttnArgs a{};
+  a.n = 1;
+  a.capacity = (int)kv->capacity;
+  a.n_head = wc.n_head_kv;
+  a.n_head_kv = wc.n_head_kv;
+  a.head_dim = wc.head_dim;
+  a.win_pad = wc.pad;
+  const AttnWindowLayout wl = attention_window_layout(a);
+  const bool valid = wc.v_id == vb->id && wc.k_ver == kb->version && wc.v_ver == vb->version;
+  if (bytes) *bytes = wc.bytes;
+  if (valid_len) *valid_len = valid ? (int64_t)wc.len : 0;
+  if (pad) *pad = wl.pad;
+  if (v_row_stride) *v_row_stride = wl.vst;
+  if (!host) return SULIMO_HIP_OK;
+  if (host_bytes < wc.bytes) return fail(kInval, "host buffer smaller than the window");
+  SULIMO_HIP_TRY(hipMemcpyAsync(host, wc.dev, wc.bytes, hipMemcpyDeviceToHost, ctx->stream));
+  return sulimo_hip_wait(ctx);
+}
+
+int32_t sulimo_hip_rope_table(sulimo_hip_ctx *ctx, size_t rope_dim, float freq_base, size_t start_pos,
+                              size_t n, sulimo_hip_buffer *table) {
+  int32_t rc = begin(ctx);
+  if (rc) return rc;
+  if (rope_dim == 0 || rope_dim % 2 != 0 || rope_dim > 512) return fail(kInval, "rope_dim must be even, 2..512");
+  if (!fits_int(start_pos + n) || !fits_int(n * rope_dim)) return fail(kInval, "rope table too large");
+  NEED(table, n * (rope_dim / 2) * 8, "table");
+  wrote(table);
+  return launch_rope_table(dp<float>(table), (int)rope_dim, freq_base, (int)start_pos, (int)n, ctx->stream);
+}
+
 // ---- whole-ubatch prefill ----
 
 int32_t sulimo_hip_execute_prefill_ubatch_ex(

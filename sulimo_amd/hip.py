@@ -176,6 +176,9 @@ def _declare(L):
         "sulimo_hip_embed_tokens": (I32, [P, P, P, P, SZ, SZ, SZ, P]),
         "sulimo_hip_kv_sync_to_host": (I32, [P, C.POINTER(KvCacheC), SZ, SZ]),
         "sulimo_hip_kv_sync_from_host": (I32, [P, C.POINTER(KvCacheC), SZ, SZ]),
+        "sulimo_hip_kv_window_download": (I32, [P, C.POINTER(KvCacheC), I32, P, SZ, C.POINTER(SZ),
+                                                C.POINTER(C.c_int64), C.POINTER(I32), C.POINTER(I32)]),
+        "sulimo_hip_rope_table": (I32, [P, SZ, F, SZ, SZ, P]),
         "sulimo_hip_set_profiling": (I32, [P, I32]),
         "sulimo_hip_get_prefill_stats": (I32, [P, C.POINTER(PrefillStats)]),
         "sulimo_hip_timer_start": (I32, [P]),
@@ -378,6 +381,11 @@ def enqueue_logits_final(ctx, x_all, scales, quants, logits, vocab_size, embd_di
                                                  vocab_size, embd_dim, token_idx))
 
 
+def rope_table(ctx, rope_dim, freq_base, start_pos, n, table):
+    """The (cos, sin) f32 pairs of a ubatch's rotations, [n][rope_dim/2][2], into table."""
+    _check(lib().sulimo_hip_rope_table(ctx.handle, rope_dim, freq_base, start_pos, n, _h(table)))
+
+
 def embed_tokens(ctx, embd_scales, embd_quants, tokens: np.ndarray, embd, vocab, x):
     t = np.ascontiguousarray(tokens, dtype=np.uint32)
     _check(lib().sulimo_hip_embed_tokens(ctx.handle, _h(embd_scales), _h(embd_quants),
@@ -501,6 +509,26 @@ class DeviceModel:
 
     def kv_host(self):
         return [b.host for b in self.kv_k], [b.host for b in self.kv_v]
+
+    def kv_window(self, layer: int):
+        """The f16 attention window kept for `layer` (sulimo_hip_kv_window_download):
+        returns (K [n_head_kv, pad, head_dim], V^T rows [n_head_kv, head_dim, v_row_stride]
+        in the stored column order, valid_len)."""
+        c = self.cfg
+        nbytes, vlen = C.c_size_t(), C.c_int64()
+        pad, vst = C.c_int32(), C.c_int32()
+        _check(lib().sulimo_hip_kv_window_download(self.ctx.handle, C.byref(self.kv), layer, None, 0,
+                                                   C.byref(nbytes), C.byref(vlen), C.byref(pad),
+                                                   C.byref(vst)))
+        raw = np.zeros(nbytes.value // 2, np.float16)
+        _check(lib().sulimo_hip_kv_window_download(self.ctx.handle, C.byref(self.kv), layer,
+                                                   raw.ctypes.data_as(C.c_void_p), raw.nbytes,
+                                                   C.byref(nbytes), C.byref(vlen), C.byref(pad),
+                                                   C.byref(vst)))
+        hkv, hd, p, s = c.n_head_kv, c.head_dim, pad.value, vst.value
+        k = raw[:hkv * p * hd].reshape(hkv, p, hd)
+        vt = raw[hkv * p * hd:hkv * p * hd + hkv * hd * s].reshape(hkv, hd, s)
+        return k, vt, int(vlen.value)
 
     def prefill_tokens(self, tokens: np.ndarray, start_pos: int = 0, ubatch: int | None = None) -> np.ndarray:
         """The engine's GPU prefill loop (engine.rs:217-286) without context repack:

@@ -6,6 +6,21 @@ repack.rs:45-80): per tensor ``scales`` f16 [rows, cols/32] and ``quants`` u8
 [0.002, 0.02] rounded to f16, norm weights 1 + N(0, 0.02) in f32, activations
 f16 N(0, 1), token ids uniform in [0, vocab). Every tensor draws from its own
 child stream of ``numpy.random.SeedSequence(seed)`` in declaration order.
+
+With those distributions every weight has mean -0.5*d, so one layer collapses the
+residual stream onto one position-independent direction and every position of a deep
+model has the same top-1 token. ``make_model(..., zero_mean=True)`` draws the same
+nibbles and scale magnitudes and gives each block's scale a random sign (the Q4_0
+format allows any f16 d): zero-mean weights, position-dependent logits. At the
+prescribed magnitudes every projection multiplies the RMS of its input by about
+0.056 * sqrt(K) (2.2 at K = 1536), attention scores have a standard deviation near 5,
+and the network amplifies rounding noise: moving 10 % of the input embeddings by one
+f16 ulp moves the fp32 reference's own residual stream by up to 0.9 (max |g - r| /
+max(|r|, 1)) after one layer. ``unit_gain=True`` scales each matrix's d range to
+[a, 10a] with a = 1 / (sqrt(21.5 * 37) * sqrt(K)), so that its weights have RMS
+1/sqrt(K) and the projection keeps the RMS of its input, as in a trained model
+(E[(q-8)^2] = 21.5, E[d^2] = 37 a^2). The benchmark keeps the prescribed distribution;
+the model-level parity tests use all three.
 """
 from __future__ import annotations
 
@@ -71,11 +86,17 @@ class Q4Tensor:
         return w.reshape(self.rows, self.cols)
 
 
-def random_q4(rng: np.random.Generator, rows: int, cols: int, d_lo=0.002, d_hi=0.02) -> Q4Tensor:
+def random_q4(rng: np.random.Generator, rows: int, cols: int, d_lo=0.002, d_hi=0.02,
+              signed: bool = False) -> Q4Tensor:
+    """Nibbles uniform in 0..15, d uniform in [d_lo, d_hi] rounded to f16. signed gives
+    every block's d a random sign, drawn after the nibbles, so the magnitudes and nibbles
+    equal those of the unsigned draw from the same generator state."""
     assert cols % 32 == 0
     nb = cols // 32
     scales = rng.uniform(d_lo, d_hi, size=(rows, nb)).astype(np.float16)
     quants = np.frombuffer(rng.bytes(rows * nb * 16), dtype=np.uint8).reshape(rows, nb, 16).copy()
+    if signed:
+        scales = np.where(rng.integers(0, 2, size=(rows, nb)) == 1, -scales, scales).astype(np.float16)
     return Q4Tensor(scales, quants)
 
 
@@ -112,27 +133,50 @@ def _norm(rng, n):
     return (1.0 + rng.normal(0.0, 0.02, size=n)).astype(np.float32)
 
 
+def unit_gain_d_range(cols: int):
+    """d range [a, 10a] for Q4_0 weights of RMS 1/sqrt(cols): RMS(q - 8) = sqrt(21.5),
+    RMS(d) = sqrt(37) * a for d uniform in [a, 10a]."""
+    a = 1.0 / (np.sqrt(21.5 * 37.0) * np.sqrt(cols))
+    return a, 10.0 * a
+
+
 def make_model(cfg: ModelConfig, seed: int, tie_embeddings: bool = True, biases: bool = False,
-               qk_norm: bool = False) -> HostModel:
+               qk_norm: bool = False, zero_mean: bool = False, unit_gain: bool = False,
+               exact_f16_weights: bool = False, qk_gain: float = 1.0) -> HostModel:
     """Random-init model. With tie_embeddings the LM head is token_embd (Qwen2.5
     ties them; the engine falls back to token_embd when output.weight is absent,
     crates/sulimo-engine/src/forward_pass.rs:58). biases adds q/k/v biases ~N(0, 0.5)
     and qk_norm per-head norm weights ~1+N(0, 0.1), from their own seed stream (the
-    other tensors are the same as without them)."""
+    other tensors are the same as without them). zero_mean gives every Q4_0 block scale
+    a random sign (same nibbles and magnitudes as without it); unit_gain (with zero_mean)
+    scales every matrix's d range to unit_gain_d_range(cols). exact_f16_weights clears
+    the low 3 mantissa bits of every d, so that every weight (q - 8) * d (at most 3
+    significant bits times 8) is an exact f16 number: an f16-operand GEMM then uses the
+    same weights as an f32 one. qk_gain multiplies the d range of the q and k projections
+    (attention scores scale with its square)."""
+    assert zero_mean or not unit_gain, "unit_gain needs zero_mean"
     ss = np.random.SeedSequence(seed)
     kids = iter(ss.spawn(4 + 9 * cfg.n_layers))
     rng = lambda: np.random.default_rng(next(kids))  # noqa: E731
+
+    def q4(r, rows, cols, gain=1.0):
+        lo, hi = unit_gain_d_range(cols) if unit_gain else (0.002, 0.02)
+        t = random_q4(r, rows, cols, gain * lo, gain * hi, signed=zero_mean)
+        if exact_f16_weights:
+            t.scales = (t.scales.view(np.uint16) & np.uint16(0xFFF8)).view(np.float16)
+        return t
+
     D, F = cfg.embd, cfg.ffn
-    token_embd = random_q4(rng(), cfg.vocab, D)
+    token_embd = q4(rng(), cfg.vocab, D)
     output_norm = _norm(rng(), D)
     out_rng = rng()
-    output = token_embd if tie_embeddings else random_q4(out_rng, cfg.vocab, D)
+    output = token_embd if tie_embeddings else q4(out_rng, cfg.vocab, D)
     layers = []
     for _ in range(cfg.n_layers):
         layers.append(HostLayer(
-            attn_norm=_norm(rng(), D), q=random_q4(rng(), cfg.q_dim, D), k=random_q4(rng(), cfg.kv_dim, D),
-            v=random_q4(rng(), cfg.kv_dim, D), o=random_q4(rng(), D, cfg.q_dim), ffn_norm=_norm(rng(), D),
-            gate=random_q4(rng(), F, D), up=random_q4(rng(), F, D), down=random_q4(rng(), D, F)))
+            attn_norm=_norm(rng(), D), q=q4(rng(), cfg.q_dim, D, qk_gain), k=q4(rng(), cfg.kv_dim, D, qk_gain),
+            v=q4(rng(), cfg.kv_dim, D), o=q4(rng(), D, cfg.q_dim), ffn_norm=_norm(rng(), D),
+            gate=q4(rng(), F, D), up=q4(rng(), F, D), down=q4(rng(), D, F)))
     if biases or qk_norm:
         er = np.random.default_rng(np.random.SeedSequence([seed, 0xB1A5]))
         for L in layers:

@@ -54,3 +54,30 @@ def kv_within_one_step(dev_ring, ref_ring, slots, bpp):
         return False
     bound = 1.05 * np.maximum(dg, dr) + 127.0 * np.abs(dg - dr) + 1e-4
     return bool(np.all(np.abs(cg * dg - cr * dr) <= bound))
+
+
+def ulp_perturb(x16, frac: float = 0.1, seed: int = 1):
+    """Moves a random `frac` of the entries of an f16 array by one ulp (up or down at
+    random): the input change used to measure how far the fp32 reference moves by
+    itself, the noise floor of a model-level comparison."""
+    x16 = np.asarray(x16, dtype=np.float16)
+    rng = np.random.default_rng(seed)
+    pick = rng.random(x16.shape) < frac
+    toward = np.where(rng.random(x16.shape) < 0.5, np.float16(np.inf), np.float16(-np.inf))
+    out = np.where(pick, np.nextafter(x16, toward), x16).astype(np.float16)
+    assert np.all(np.isfinite(out))
+    return out
+
+
+def normwise_err(got, ref) -> float:
+    """||g - r|| / ||r|| over all elements."""
+    g = np.asarray(got, dtype=np.float64).ravel()
+    r = np.asarray(ref, dtype=np.float64).ravel()
+    return float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30))
+
+
+def ring_values(ring, slots, bpp):
+    """f32 values code * f16(d) of the Q8_0 ring blocks at `slots` (kv_cache.rs layout)."""
+    b = np.asarray(ring).reshape(-1, bpp)[slots].reshape(-1, 34)
+    d = b[:, :2].copy().view(np.float16).astype(np.float32)
+    return b[:, 2:].view(np.int8).astype(np.float32) * d

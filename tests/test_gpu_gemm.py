@@ -78,16 +78,21 @@ SHAPES = {  # (K, N) of the Qwen2.5-1.5B layer linears, and the Llama-3.2-3B QKV
 }
 
 
+EDGE_M = (37, 1000, 3071)  # the non-tile-multiple token counts of the edge-shape stress
+
+
 @pytest.mark.parametrize("M,name", [(128, "gate_up"), (512, "q_o"), (512, "k_v"), (512, "gate_up"),
-                                    (512, "down"), (37, "gate_up"), (1000, "q_o"), (3071, "k_v"),
-                                    (1, "down"), (8, "q_o"), (1536, "down"), (1536, "l3b_qkv")])
+                                    (512, "down"), (1, "down"), (8, "q_o"), (1536, "down"),
+                                    (1536, "l3b_qkv")]
+                         + [(M, name) for M in EDGE_M for name in ("q_o", "k_v", "gate_up", "down")])
 def test_benchmark_shapes_vs_fp32(ctx, M, name):
     """Benchmark shapes (nibbles uniform, d in [0.002, 0.02], x ~ N(0,1)) against an
     fp32 reference: max rel err <= 1e-2 (denominator max(|ref|,1)). The shapes cover the
     planner's tiles: 32 x 128 with four K parts inside the workgroup (M <= 512 q/o/k/v),
     64 x 128 with and without two parts (gate/up at M = 128 and 512, q/o at M = 1000),
     K splits across workgroups (down at M = 512), and 128 x 256 with two parts (down,
-    also split across workgroups, and the Llama QKV at M = 1536)."""
+    also split across workgroups, and the Llama QKV at M = 1536). All four layer shapes
+    run at each of M = 37, 1000 and 3071, where the last token tile is partly empty."""
     K, N = SHAPES[name]
     rng = np.random.default_rng(1000 + M + K + N)
     w = S.random_q4(rng, N, K)

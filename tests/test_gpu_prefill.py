@@ -13,7 +13,7 @@ import pytest
 import oracle
 from sulimo_amd import hip
 from sulimo_amd import synthetic as S
-from tests.helpers import cosine, kv_within_one_step
+from tests.helpers import cosine, kv_within_one_step, ulp_perturb
 
 pytestmark = pytest.mark.gpu
 
@@ -247,18 +247,46 @@ def test_resume_at_1536_with_wrap_at_2048():
     dm.release()
 
 
-def test_all_positions_top1_agreement():
-    """All-positions LM-head validation mode: device argmax per position equals the
-    oracle's top-1 on >= 99.5 % of positions; logits within 1e-2 of their scale."""
-    cfg = S.ModelConfig(2, 512, 1024, 8, 2, 64, 64, 2048, 1e6, 1e-6, 1)
-    dm, okv, res = run_both(cfg, 44, [96, 64], 256, all_logits=True)
-    agree, total = 0, 0
+@pytest.mark.parametrize("weights", ["prescribed", "zero_mean"])
+def test_all_positions_top1_agreement(weights):
+    """All-positions LM-head validation mode: device argmax per position against the
+    oracle's top-1, logits within 1e-2 of their scale. On the prescribed weights
+    (positive scales) every position has nearly the same top-1, and agreement must be
+    >= 99.5 %. The zero-mean variant (random-sign scales) gives distinct top-1 tokens at
+    >= 90 % of positions, so that agreement measures something; there the oracle itself,
+    fed the same embeddings with 10 % of them moved by one f16 ulp, keeps only about
+    98 % of its top-1 tokens, and the device must reach 99.5 % or that floor less its
+    sampling error."""
+    zero_mean = weights == "zero_mean"
+    cfg = S.ModelConfig(2, 512, 1024, 8, 2, 64, 64, 8192, 1e6, 1e-6, 1)
+    dm, okv, res = run_both(cfg, 44, [96, 64], 256, all_logits=True, zero_mean=zero_mean)
+    agree, total, r_args = 0, 0, []
     for _, g_all, g_arg, r_all in res:
         assert np.max(np.abs(g_all - r_all)) <= 1e-2 * float(np.abs(r_all).max())
         assert np.array_equal(g_arg, np.argmax(g_all, axis=1))
-        agree += int(np.sum(g_arg == np.argmax(r_all, axis=1)))
+        r_args.append(np.argmax(r_all, axis=1))
+        agree += int(np.sum(g_arg == r_args[-1]))
         total += g_arg.size
-    assert agree / total >= 0.995
+    distinct = len(set(np.concatenate(r_args).tolist())) / total
+    bar = 0.995
+    if zero_mean:
+        # the oracle's floor: the same two chunks on one-ulp-perturbed embeddings
+        hm = S.make_model(cfg, 44, zero_mean=True)
+        toks = S.random_tokens(45, 160, cfg.vocab)
+        om, pkv = oracle.OracleModel(hm), oracle.OracleKv(cfg, 256)
+        kept = 0
+        for pos, m in ((0, 96), (96, 64)):
+            p_all = oracle.prefill_reference(om, pkv, ulp_perturb(S.embed_host(hm, toks[pos:pos + m])), pos,
+                                             all_logits=True)
+            kept += int(np.sum(np.argmax(p_all, axis=1) == r_args[0 if pos == 0 else 1]))
+        floor = kept / total
+        bar = min(0.995, floor - 2.0 * np.sqrt(floor * (1.0 - floor) / total) - 1.0 / total)
+        print(f"all-positions top-1: oracle floor {floor:.4%}")
+    print(f"all-positions top-1: agreement {agree / total:.4%} (bar {bar:.4%}), oracle top-1 distinct at "
+          f"{distinct:.2%}")
+    if zero_mean:
+        assert distinct >= 0.9
+    assert agree / total >= bar
     dm.release()
 
 

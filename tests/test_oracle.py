@@ -339,9 +339,10 @@ def test_kv_store_cl_matches_quantize():
 
 # ---- whole model ----
 
-def _textbook_prefill(hm, x16, n):
+def _textbook_prefill(hm, x16, n, states=False):
     """Float64 textbook transformer with the device op order; K/V pass through the
-    oracle's Q8_0 codec (the cache format), everything else unrounded."""
+    oracle's Q8_0 codec (the cache format), everything else unrounded. states: also
+    return the output-normed rows and the final residual stream."""
     c = hm.cfg
     x = x16.astype(np.float64)
     D, hd = c.embd, c.head_dim
@@ -390,7 +391,26 @@ def _textbook_prefill(hm, x16, n):
         up = h @ L.up.dequant_f32().T.astype(np.float64)
         x = x + (gt / (1 + np.exp(-gt)) * up) @ L.down.dequant_f32().T.astype(np.float64)
     h = rms(x, hm.output_norm)
-    return h @ hm.output.dequant_f32().T.astype(np.float64)
+    logits = h @ hm.output.dequant_f32().T.astype(np.float64)
+    return (logits, h, x) if states else logits
+
+
+@pytest.mark.parametrize("weights", [dict(), dict(zero_mean=True, unit_gain=True)], ids=["prescribed", "unit_gain"])
+def test_prefill_reference_hidden_states_vs_textbook(weights):
+    """The oracle's final residual stream and output-normed rows (the device's scratch.x
+    and scratch.h) against the float64 textbook: within 1e-2 normwise, and h_final is
+    the output RMSNorm of x_final."""
+    cfg = S.ModelConfig(2, 128, 256, 4, 2, 32, 32, 96, 10000.0, 1e-6, 1)
+    hm = S.make_model(cfg, 5, **weights)
+    x = S.embed_host(hm, S.random_tokens(6, 12, cfg.vocab))
+    lg, h, xf = oracle.prefill_reference(oracle.OracleModel(hm), oracle.OracleKv(cfg, 32), x, 0, all_logits=True,
+                                         want_h=True, want_x=True)
+    rl, rh, rx = _textbook_prefill(hm, x, 12, states=True)
+    assert np.linalg.norm(xf - rx) <= 1e-2 * np.linalg.norm(rx)
+    assert np.linalg.norm(h - rh) <= 1e-2 * np.linalg.norm(rh)
+    assert np.max(np.abs(lg - rl)) <= 2e-2 * np.abs(rl).max()
+    want_h = np.stack([oracle.rmsnorm(r, hm.output_norm, cfg.eps) for r in xf])
+    assert np.array_equal(h.view(np.uint32), want_h.view(np.uint32))
 
 
 @pytest.mark.parametrize("extras", [False, True], ids=["plain", "bias_qknorm"])
