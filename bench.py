@@ -4,9 +4,14 @@ random-init Qwen2.5-1.5B-shaped Q4_0 model (28 layers, hidden 1536, 12/2 heads,
 head_dim 128, FFN 8960, vocab 151936, Q8_0 KV ring of 2048 positions, last-token
 logits), plus the Q4_0 GEMM throughput at the one-layer M=512 shapes.
 
-One step = device embedding gather of the 2048 prompt ids + execute_prefill_ubatch
-(all 28 layers, final norm, LM head of the last token) ending in its blocking
-wait; weights, KV ring and scratch are resident in HBM before timing starts.
+One step = device embedding gather of the 2048 prompt ids (2 bytes per token up) +
+execute_prefill_ubatch (all 28 layers, final norm, LM head of the last token) ending in
+its blocking wait + the read of the f32 last-token logits into their host mirror (the
+engine's map_read after every prompt, crates/sulimo-engine/src/engine.rs:273-283): the
+wall from the prompt upload to the logits on the host. Weights, KV ring and scratch are
+resident in HBM before timing starts. The library replays each ubatch's launches from
+captured HIP graphs (its default); extra.eager_launches is the same step with every
+kernel launched one by one, extra.device_resident the step without the logits read.
 
 Prints one JSON line. Before the W warm-up steps, untimed steps run for at least
 half a second so that the GPU clock has left its idle state (counted under
@@ -15,7 +20,9 @@ stream; extra.ubatch512 is the same prompt in the reference's default micro-batc
 of 512 tokens, and extra.layer_m512_fused the per-layer time of their Q4_0 linears as
 the prefill runs them (QKV with the RoPE + KV-store epilogue, o, gate/up with SwiGLU,
 down with its residual + norm reduction). `roofline` is the Q4_0 GEMM kernel (the
-dominant kernel: the gate/up projection with its SwiGLU epilogue), with its per-launch
+dominant kernel: the gate/up projection with its SwiGLU epilogue; extra.gemm_all_roofline
+is the same figure over every GEMM launch of the step, the definition `roofline` had
+before it covered the dominant kernel alone), with its per-launch
 GPU time taken from a hipEvent pair that each of its launches stamps with the kernel's
 own start and end (hipExtLaunchKernelGGL) over K more identical steps (the other
 launches of those steps sit between recorded events, which slow the steps, so they
@@ -226,13 +233,26 @@ def main():
     tokens = S.random_tokens(SEED_TOKENS, T, cfg.vocab)
     dm = hip.DeviceModel(ctx, hm, capacity=T, max_n=min(a.ubatch, T))
 
-    def step():
+    logits_buf = dm.scratch_bufs["logits"]
+
+    def step(read_logits=True):
         pos = 0
         while pos < T:
             m = min(a.ubatch, T - pos)
             dm.embed(tokens[pos:pos + m])
             dm.execute_prefill_ubatch(pos, m)
             pos += m
+        if read_logits:
+            logits_buf.map_read()  # blocking D2H of the last-token logits into the host mirror
+            logits_buf.unmap()
+
+    def timed_steps(**kw):
+        ctx.wait()
+        t = time.perf_counter()
+        for _ in range(a.steps):
+            step(**kw)
+        ctx.wait()
+        return time.perf_counter() - t
 
     # The GPU clock ramps up from idle over a few hundred ms: untimed steps for at least
     # PREWARM_S (counted in the output) before the W warm-up steps proper.
@@ -246,14 +266,16 @@ def main():
     ctx.wait()
 
     # Timed region: K steps, nothing but the prefill on the stream.
-    ctx.wait()
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        step()
-    ctx.wait()
-    wall = time.perf_counter() - t0
+    wall = timed_steps()
     ms_per_step = wall / a.steps * 1e3
     value = T * a.steps / wall
+    # The same steps without the logits read, and with eager launches instead of replay.
+    wall_dev = timed_steps(read_logits=False)
+    ctx.set_graph_replay(False)
+    for _ in range(a.warmup):
+        step()
+    wall_eager = timed_steps()
+    ctx.set_graph_replay(True)
 
     # Kernel timing: the same K steps again with a hipEvent pair per launch on the
     # library's stream. The GEMM kernels stamp their pair with their own start and end
@@ -292,7 +314,20 @@ def main():
                 if k.total_ms > 0 and k.flop > 0 else None,
                 "gbs": round(k.bytes / (k.total_ms * 1e-3) / 1e9, 1) if k.total_ms > 0 else None}
 
-    extra = {"kernel_classes": {"gemm": cls(st.gemm), "gemm_qkv": cls(st.gemm_qkv), "gemm_o": cls(st.gemm_o),
+    gall = st.gemm
+    gall_tf = gall.flop / (gall.total_ms * 1e-3) / 1e12 if gall.total_ms > 0 else 0.0
+    extra = {"device_resident": {"value": round(T * a.steps / wall_dev, 1), "unit": "tokens/s",
+                                 "ms_per_step": round(wall_dev / a.steps * 1e3, 3),
+                                 "note": "the step without the last-token logits read"},
+             "eager_launches": {"value": round(T * a.steps / wall_eager, 1), "unit": "tokens/s",
+                                "ms_per_step": round(wall_eager / a.steps * 1e3, 3),
+                                "note": "the step with graph replay off (every kernel launched one by one)"},
+             "gemm_all_roofline": {"achieved": round(gall_tf, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+                                   "frac": round(gall_tf / PEAK_F16_TFLOPS, 4),
+                                   "launches_per_step": int(gall.launches // max(a.steps, 1)),
+                                   "note": "every Q4_0 GEMM launch of the step (QKV, o, gate/up, down with "
+                                           "their K-split reductions, LM head), stamped kernel times"},
+             "kernel_classes": {"gemm": cls(st.gemm), "gemm_qkv": cls(st.gemm_qkv), "gemm_o": cls(st.gemm_o),
                                 "gemm_gate_up": cls(st.gemm_gate_up), "gemm_down": cls(st.gemm_down),
                                 "gemm_lm_head": cls(st.gemm_lm_head), "attention": cls(st.attention),
                                 "norm": cls(st.norm), "rope_kv": cls(st.rope_kv),
@@ -310,6 +345,8 @@ def main():
                 m = min(512, T - pos)
                 dm.embed(tokens[pos:pos + m])
                 dm.execute_prefill_ubatch(pos, m)
+            logits_buf.map_read()
+            logits_buf.unmap()
         for _ in range(a.warmup):
             step512()
         ctx.wait()

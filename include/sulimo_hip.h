@@ -144,8 +144,10 @@ int32_t sulimo_hip_enqueue_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_b
  * in a static device array of 64 MiB that every GPU the library runs on holds until
  * the process ends. Matrices whose layout exceeds it (m * k * 18/32 bytes, rounded up
  * to 32 rows and 64 columns) are rejected with SULIMO_HIP_ERR_INVALID_ARGUMENT. All
- * calls on one GPU share that array: calls that overlap on one GPU (two contexts'
- * streams running at once) race and must not be issued. */
+ * calls on one GPU share that array, so the library orders them: each call's stream
+ * first waits for an event the previous no-alloc call on that GPU recorded, from
+ * whichever context or thread it came. Calls from two streams therefore run one after
+ * the other, never at once. */
 int32_t sulimo_hip_enqueue_gemm_q4_0_f16_noalloc(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
                                                  const sulimo_hip_buffer *quants,
                                                  const sulimo_hip_buffer *x, sulimo_hip_buffer *out,
@@ -369,6 +371,16 @@ typedef struct {
 
 /* Turns per-launch event timing on or off and clears the statistics. */
 int32_t sulimo_hip_set_profiling(sulimo_hip_ctx *ctx, int32_t enable);
+
+/* Graph replay of execute_prefill_ubatch (no counterpart in the reference; on by
+ * default). The first call with a given set of shapes, buffers and kept-window state
+ * captures its launches into two HIP graphs, split where the wake-up of the final wait
+ * is gated; later identical calls replay them, which costs the engine thread a few
+ * microseconds of CPU instead of one launch each (the reference's engine thread must
+ * stay under 5 % of a core while the GPU runs a prefill). Calls with profiling on or
+ * with per-position outputs run eagerly. Results are bit-identical either way.
+ * Disabling it also frees the cached graphs. */
+int32_t sulimo_hip_set_graph_replay(sulimo_hip_ctx *ctx, int32_t enable);
 int32_t sulimo_hip_get_prefill_stats(const sulimo_hip_ctx *ctx, sulimo_hip_prefill_stats *out);
 
 /* Record a start event on the context stream; stop records the end event, waits for

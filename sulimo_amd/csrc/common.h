@@ -36,6 +36,15 @@ struct ParkSlot {
   uint64_t posted = 0;
 };
 
+// A ubatch's launches captured once and replayed: two executable graphs split at the
+// wake-up gate (the host records near_event between them), keyed by every value the
+// launches were built from.
+struct PrefillGraph {
+  std::vector<uint64_t> key;
+  hipGraphExec_t pre = nullptr, post = nullptr;
+  uint64_t last_use = 0;
+};
+
 struct sulimo_hip_ctx {
   int device = 0;
   bool shared = false;  // the get_or_init singleton (never freed)
@@ -66,6 +75,10 @@ struct sulimo_hip_ctx {
   std::vector<hipEvent_t> ev_pool;  // pairs: [2i] start, [2i+1] end
   std::vector<ProfRecord> pending;
   sulimo_hip_prefill_stats stats{};
+  // Graph replay of execute_prefill_ubatch (sulimo_hip_set_graph_replay).
+  bool graph_replay = true;
+  std::vector<PrefillGraph> graphs;
+  uint64_t graph_tick = 0;
 };
 
 // GEMM-layout copy of one Q4_0 matrix (or an interleaved gate/up pair), built from
@@ -235,12 +248,23 @@ size_t gemm_q4_0_workspace_bytes(const GemmArgs &a);
 // Size of the static device scratch array of the no-alloc GEMM entry point (one per
 // device, held until the process ends).
 constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+// Orders the no-alloc GEMM calls of every context on one device: each call's stream
+// waits for the event the previous call recorded (under the mutex), so that one call's
+// panel pack cannot overwrite weights that another call's GEMM still reads.
+struct NoAllocOrder {
+  std::mutex m;
+  hipEvent_t ev = nullptr;
+};
+// The device's NoAllocOrder (its event created with the scratch address), or null.
+NoAllocOrder *noalloc_order(int device);
 
 // Blocks the calling thread until all work queued on ctx->stream is done, without
 // spinning while the GPU runs: the thread sleeps until a host function enqueued after
 // `gate` (an event already recorded on ctx->stream; null = the end of the queue)
 // wakes it, then waits for the rest of the queue. Reports asynchronous failures.
 int32_t wait_parked(sulimo_hip_ctx *ctx, hipEvent_t gate);
+// Destroys the context's cached prefill graphs.
+void drop_prefill_graphs(sulimo_hip_ctx *ctx);
 
 // The RoPE rotation terms a*b - c*d and a*b + c*d with both products rounded to f32
 // before the add (no fused multiply-add), as the reference's rope_f16 and

@@ -169,6 +169,11 @@ int32_t sulimo_hip_enqueue_gemm_q4_0_f16_noalloc(sulimo_hip_ctx *ctx, const suli
     return fail(kInval, "the no-alloc GEMM holds at most " + std::to_string(kNoAllocScratchBytes) +
                             " bytes of weights in its GEMM layout; this matrix needs " + std::to_string(pan));
   if (n == 0) return SULIMO_HIP_OK;
+  NoAllocOrder *order = noalloc_order(ctx->device);
+  if (!order) return fail(SULIMO_HIP_ERR_DRIVER, "the no-alloc ordering event was not created");
+  // After the previous no-alloc call on this device, from whatever stream it came.
+  std::lock_guard<std::mutex> serial(order->m);
+  SULIMO_HIP_TRY(hipStreamWaitEvent(ctx->stream, order->ev, 0));
   wrote(out);
   uint8_t *scr = reinterpret_cast<uint8_t *>(ctx->scratch);
   if ((rc = launch_pack_q4_panels(dp<const uint16_t>(scales), dp<const uint8_t>(quants), nullptr, nullptr, (int)m,
@@ -184,7 +189,9 @@ int32_t sulimo_hip_enqueue_gemm_q4_0_f16_noalloc(sulimo_hip_ctx *ctx, const suli
   a.nseg = 1;
   a.part = reinterpret_cast<float *>(scr + pan_al);
   a.part_bytes = kNoAllocScratchBytes - pan_al;
-  return launch_gemm_q4_0(a, ctx->stream);
+  if ((rc = launch_gemm_q4_0(a, ctx->stream))) return rc;
+  SULIMO_HIP_TRY(hipEventRecord(order->ev, ctx->stream));
+  return SULIMO_HIP_OK;
 }
 
 int32_t sulimo_hip_gemm_q4_0_f16(sulimo_hip_ctx *ctx, const sulimo_hip_buffer *scales,
@@ -626,6 +633,33 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     wrote(outputs->logits_all);
     wrote(outputs->argmax_all);
   }
+  // Panel copies of every layer's weights and of the LM head (built by the first
+  // ubatch), resolved before the first launch so that no allocation or panel build
+  // falls inside a graph capture.
+  std::vector<const uint8_t *> panels(6 * L);
+  const uint8_t *lm_panel = nullptr;
+  for (size_t l = 0; l < L; l++) {
+    const sulimo_hip_layer_tensors &T = tensors->layers[l];
+    const uint8_t **pp = &panels[6 * l];
+    if ((rc = get_q4_panels(ctx, T.attn_q_scales, T.attn_q_quants, nullptr, nullptr, (int)qd, (int)D, &pp[0])) ||
+        (rc = get_q4_panels(ctx, T.attn_k_scales, T.attn_k_quants, nullptr, nullptr, (int)kvd, (int)D, &pp[1])) ||
+        (rc = get_q4_panels(ctx, T.attn_v_scales, T.attn_v_quants, nullptr, nullptr, (int)kvd, (int)D, &pp[2])) ||
+        (rc = get_q4_panels(ctx, T.attn_out_scales, T.attn_out_quants, nullptr, nullptr, (int)D, (int)qd, &pp[3])) ||
+        (rc = get_q4_panels(ctx, T.ffn_gate_scales, T.ffn_gate_quants, T.ffn_up_scales, T.ffn_up_quants, (int)F,
+                            (int)D, &pp[4])) ||
+        (rc = get_q4_panels(ctx, T.ffn_down_scales, T.ffn_down_quants, nullptr, nullptr, (int)D, (int)F, &pp[5])))
+      return rc;
+  }
+  if ((rc = get_q4_panels(ctx, tensors->output_scales, tensors->output_quants, nullptr, nullptr, (int)V, (int)D,
+                          &lm_panel)))
+    return rc;
+  const bool want_outputs = outputs && (outputs->logits_all || outputs->argmax_all || outputs->unfused);
+
+  // Every launch of the ubatch, in order. gate() runs where the wake-up of the final
+  // wait is gated (before the last down projection): it records near_event, or, under
+  // graph capture, closes the first graph and opens the second.
+  auto body = [&](auto &&gate) -> int32_t {
+  int32_t rc = SULIMO_HIP_OK;
   if ((rc = timed(ctx, PROF_NORM, 0, 6.0 * n * D, [&] { return launch_f16_to_f32(dp<const uint16_t>(scratch->x), xres, n * D, s); }))) return rc;
   float *rope_tab = reinterpret_cast<float *>(ws + off_r);
   if ((rc = timed(ctx, PROF_ROPE_KV, 0, 8.0 * n * (cfg->rope_dim / 2), [&] {
@@ -646,16 +680,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
                                                  nullptr, (int)D, cfg->eps, in, s);
                      })))
       return rc;
-    // panel copies of this layer's weights (built on the first ubatch)
-    const uint8_t *pq, *pk, *pv, *po, *pgu, *pd;
-    if ((rc = get_q4_panels(ctx, T.attn_q_scales, T.attn_q_quants, nullptr, nullptr, (int)qd, (int)D, &pq)) ||
-        (rc = get_q4_panels(ctx, T.attn_k_scales, T.attn_k_quants, nullptr, nullptr, (int)kvd, (int)D, &pk)) ||
-        (rc = get_q4_panels(ctx, T.attn_v_scales, T.attn_v_quants, nullptr, nullptr, (int)kvd, (int)D, &pv)) ||
-        (rc = get_q4_panels(ctx, T.attn_out_scales, T.attn_out_quants, nullptr, nullptr, (int)D, (int)qd, &po)) ||
-        (rc = get_q4_panels(ctx, T.ffn_gate_scales, T.ffn_gate_quants, T.ffn_up_scales, T.ffn_up_quants, (int)F,
-                            (int)D, &pgu)) ||
-        (rc = get_q4_panels(ctx, T.ffn_down_scales, T.ffn_down_quants, nullptr, nullptr, (int)D, (int)F, &pd)))
-      return rc;
+    const uint8_t *pq = panels[6 * l], *pk = panels[6 * l + 1], *pv = panels[6 * l + 2],
+                  *po = panels[6 * l + 3], *pgu = panels[6 * l + 4], *pd = panels[6 * l + 5];
     // attention arguments first: the RoPE + Q8_0 store also writes the f16 window
     // entries of the new positions
     AttnArgs at{};
@@ -807,7 +833,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     gd.part_bytes = gemm_ws;
     const bool last = l + 1 == L;
     // the wake-up of the final wait is gated here, some 50-100 us before the end
-    if (last) SULIMO_HIP_TRY(hipEventRecord(ctx->near_event, s));
+    if (last && (rc = gate())) return rc;
     gd.norm_w = dp<const float>(last ? tensors->output_norm : tensors->layers[l + 1].attn_norm);
     gd.norm_out = dp<uint16_t>(scratch->h);
     gd.norm_x16 = last ? dp<uint16_t>(scratch->x) : nullptr;
@@ -852,8 +878,97 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
         return rc;
     }
   }
+  return SULIMO_HIP_OK;
+  };
+
+  if (!ctx->graph_replay || ctx->prof || want_outputs) {
+    // Eager launches. With per-position outputs the LM head over all rows follows the
+    // gate point, so the wake-up is not gated (the host function ends the queue).
+    rc = body([&]() -> int32_t {
+      if (!want_outputs) SULIMO_HIP_TRY(hipEventRecord(ctx->near_event, s));
+      return SULIMO_HIP_OK;
+    });
+    if (rc) return rc;
+  } else {
+    // Graph replay: the key holds every value the launches are built from.
+    std::vector<uint64_t> key;
+    auto put = [&](uint64_t v) { key.push_back(v); };
+    auto putp = [&](const void *p) { key.push_back((uint64_t)(uintptr_t)p); };
+    auto putf = [&](float f) {
+      uint32_t u;
+      memcpy(&u, &f, 4);
+      key.push_back(u);
+    };
+    put(L); put(D); put(F); put(Hq); put(Hkv); put(hd); put((uint64_t)cfg->rope_dim); put(V);
+    put((uint64_t)cfg->rope_mode); putf(cfg->rope_base); putf(cfg->eps);
+    put(start_pos); put(n); put(cap);
+    putp(ws); put(gemm_ws); putp(lm_panel); putp(tensors->output_norm->dev);
+    for (sulimo_hip_buffer *b : {scratch->x, scratch->h, scratch->q, scratch->k, scratch->v, scratch->attn_out,
+                                 scratch->ffn_swiglu, scratch->logits})
+      putp(b->dev);
+    for (size_t l = 0; l < L; l++) {
+      const sulimo_hip_layer_tensors &T = tensors->layers[l];
+      for (int i = 0; i < 6; i++) putp(panels[6 * l + i]);
+      putp(T.attn_norm->dev); putp(T.ffn_norm->dev);
+      putp(opt_f32(T.attn_q_bias)); putp(opt_f32(T.attn_k_bias)); putp(opt_f32(T.attn_v_bias));
+      putp(opt_f32(T.attn_q_norm)); putp(opt_f32(T.attn_k_norm));
+      putp(kv->k_buffers[l]->dev); putp(kv->v_buffers[l]->dev);
+      if (keep_win) {
+        putp(kv->k_buffers[l]->kvwin.dev);
+        put((uint64_t)kv->k_buffers[l]->kvwin.pad);
+        put((uint64_t)win_valid[l]);
+      }
+    }
+    PrefillGraph *hit = nullptr;
+    for (PrefillGraph &g : ctx->graphs)
+      if (g.key == key) hit = &g;
+    if (!hit) {
+      hipGraph_t g1 = nullptr, g2 = nullptr;
+      SULIMO_HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      bool split = false;
+      int32_t brc = body([&]() -> int32_t {
+        hipError_t e = hipStreamEndCapture(s, &g1);
+        if (e != hipSuccess) return hip_fail(e, "graph capture");
+        e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) return hip_fail(e, "graph capture");
+        split = true;
+        return SULIMO_HIP_OK;
+      });
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      hipError_t ce = hipStreamIsCapturing(s, &cs);
+      if (ce == hipSuccess && cs != hipStreamCaptureStatusNone) ce = hipStreamEndCapture(s, &g2);
+      PrefillGraph pg;
+      pg.key = std::move(key);
+      if (brc == SULIMO_HIP_OK && ce == hipSuccess && split && g1 && g2) {
+        ce = hipGraphInstantiate(&pg.pre, g1, nullptr, nullptr, 0);
+        if (ce == hipSuccess) ce = hipGraphInstantiate(&pg.post, g2, nullptr, nullptr, 0);
+      } else if (brc == SULIMO_HIP_OK && ce == hipSuccess) {
+        ce = hipErrorInvalidValue;
+      }
+      if (g1) hipGraphDestroy(g1);
+      if (g2) hipGraphDestroy(g2);
+      if (brc || ce != hipSuccess) {
+        if (pg.pre) hipGraphExecDestroy(pg.pre);
+        if (pg.post) hipGraphExecDestroy(pg.post);
+        return brc ? brc : hip_fail(ce, "prefill graph capture");
+      }
+      if (ctx->graphs.size() >= 8) {  // evict the least recently used
+        auto lru = std::min_element(ctx->graphs.begin(), ctx->graphs.end(),
+                                    [](const PrefillGraph &a, const PrefillGraph &b) { return a.last_use < b.last_use; });
+        hipGraphExecDestroy(lru->pre);
+        hipGraphExecDestroy(lru->post);
+        ctx->graphs.erase(lru);
+      }
+      ctx->graphs.push_back(std::move(pg));
+      hit = &ctx->graphs.back();
+    }
+    hit->last_use = ++ctx->graph_tick;
+    SULIMO_HIP_TRY(hipGraphLaunch(hit->pre, s));
+    SULIMO_HIP_TRY(hipEventRecord(ctx->near_event, s));
+    SULIMO_HIP_TRY(hipGraphLaunch(hit->post, s));
+  }
   // 15. one wait for the whole ubatch (the thread sleeps while the GPU works)
-  rc = wait_parked(ctx, ctx->near_event);
+  rc = wait_parked(ctx, want_outputs ? nullptr : ctx->near_event);
   if (rc == SULIMO_HIP_OK && keep_win) {
     for (size_t l = 0; l < L; l++) {  // the kept windows now hold positions [0, start_pos + n)
       KvWindowCache &wc = kv->k_buffers[l]->kvwin;

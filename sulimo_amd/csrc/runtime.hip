@@ -8,6 +8,8 @@
 #include <mutex>
 #include <string>
 
+#include <chrono>
+
 #include "common.h"
 
 namespace sulimo {
@@ -132,15 +134,26 @@ static int32_t fill_info(int device, sulimo_hip_device_info *info) {
 // array's name on the host is not a device address).
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
-// Per-device address of `scratch`, resolved once per device with that device current.
+static NoAllocOrder g_noalloc_order[64];
+
+NoAllocOrder *noalloc_order(int device) {
+  return device >= 0 && device < 64 && g_noalloc_order[device].ev ? &g_noalloc_order[device] : nullptr;
+}
+
+// Per-device address of `scratch`, resolved once per device with that device current,
+// and the event that orders the no-alloc calls on it.
 static int32_t resolve_scratch(int device, void **out) {
   static std::mutex mu;
   static void *ptrs[64] = {nullptr};
   std::lock_guard<std::mutex> g(mu);
   if (!ptrs[device]) {
     void *p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "scratch symbol address");
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, "no-alloc ordering event");
+    g_noalloc_order[device].ev = ev;
     ptrs[device] = p;
   }
   *out = ptrs[device];
@@ -190,6 +203,14 @@ static int32_t create_ctx(int device, bool shared, sulimo_hip_ctx **out) {
   return SULIMO_HIP_OK;
 }
 
+void drop_prefill_graphs(sulimo_hip_ctx *ctx) {
+  for (PrefillGraph &g : ctx->graphs) {
+    if (g.pre) hipGraphExecDestroy(g.pre);
+    if (g.post) hipGraphExecDestroy(g.post);
+  }
+  ctx->graphs.clear();
+}
+
 // Host function run by the HIP runtime on the waiter stream.
 static void park_post(void *p) {
   ParkSlot *k = static_cast<ParkSlot *>(p);
@@ -221,8 +242,16 @@ int32_t wait_parked(sulimo_hip_ctx *ctx, hipEvent_t gate) {
     }
     if (e == hipSuccess) e = hipLaunchHostFunc(hs, park_post, &ctx->park);
     if (e == hipSuccess) {
+      // Sleep until the host function runs. Every 10 ms the thread also asks the
+      // runtime about the end event: a stream that failed never runs the host
+      // function, and the error is reported instead of waiting for ever.
       std::unique_lock<std::mutex> l(ctx->park.m);
-      ctx->park.cv.wait(l, [&] { return ctx->park.posted >= want; });
+      while (!ctx->park.cv.wait_for(l, std::chrono::milliseconds(10),
+                                    [&] { return ctx->park.posted >= want; })) {
+        const hipError_t q = hipEventQuery(ctx->done_event);
+        if (q != hipSuccess && q != hipErrorNotReady) return hip_fail(q, "stream execution");
+        if (q == hipSuccess) break;  // finished; the host function may still be on its way
+      }
     } else {
       ctx->park_want--;  // no host function queued: fall back to the runtime's wait
     }
@@ -273,6 +302,7 @@ int32_t sulimo_hip_context_release(sulimo_hip_ctx *ctx) {
   hipEventDestroy(ctx->t0);
   hipEventDestroy(ctx->t1);
   for (hipEvent_t e : ctx->ev_pool) hipEventDestroy(e);
+  drop_prefill_graphs(ctx);
   hipStreamDestroy(ctx->stream);
   hipStreamDestroy(ctx->side);
   delete ctx;
@@ -312,6 +342,15 @@ int32_t sulimo_hip_probe(sulimo_hip_probe_result *out) {
 int32_t sulimo_hip_wait(sulimo_hip_ctx *ctx) {
   if (!ctx) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "ctx is null");
   return wait_parked(ctx, nullptr);
+}
+
+int32_t sulimo_hip_set_graph_replay(sulimo_hip_ctx *ctx, int32_t enable) {
+  if (!ctx) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "ctx is null");
+  int32_t rc = sulimo_hip_wait(ctx);
+  if (rc) return rc;
+  ctx->graph_replay = enable != 0;
+  if (!ctx->graph_replay) drop_prefill_graphs(ctx);
+  return SULIMO_HIP_OK;
 }
 
 int32_t sulimo_hip_set_profiling(sulimo_hip_ctx *ctx, int32_t enable) {

@@ -180,6 +180,7 @@ def _declare(L):
                                                 C.POINTER(C.c_int64), C.POINTER(I32), C.POINTER(I32)]),
         "sulimo_hip_rope_table": (I32, [P, SZ, F, SZ, SZ, P]),
         "sulimo_hip_set_profiling": (I32, [P, I32]),
+        "sulimo_hip_set_graph_replay": (I32, [P, I32]),
         "sulimo_hip_get_prefill_stats": (I32, [P, C.POINTER(PrefillStats)]),
         "sulimo_hip_timer_start": (I32, [P]),
         "sulimo_hip_timer_stop": (I32, [P, C.POINTER(C.c_float)]),
@@ -243,6 +244,9 @@ class HipContext:
         i = DeviceInfo()
         _check(lib().sulimo_hip_get_device_info(self.handle, C.byref(i)))
         return i
+
+    def set_graph_replay(self, enable: bool):
+        _check(lib().sulimo_hip_set_graph_replay(self.handle, 1 if enable else 0))
 
     def set_profiling(self, enable: bool):
         """Per-launch hipEvent timing of execute_prefill_ubatch (clears the statistics)."""

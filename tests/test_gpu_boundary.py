@@ -44,8 +44,10 @@ def test_zero_spin_waiter(ctx):
 
 def test_prefill_call_cpu_share(ctx):
     """CPU time of the engine thread over one whole 2048-token prefill call of the
-    Qwen2.5-1.5B-shaped model (28 layers): the launches themselves cost CPU, waiting
-    for them must not. Reported, and the thread must sleep through most of the call."""
+    Qwen2.5-1.5B-shaped model (28 layers): at most 5 % of the call's wall time, the
+    reference's acceptance for GPU prefill ("CPU utilization of engine process <= 5% of
+    one core", SULIMO_GEN8_10_BUILD_PLAN.md:383). The call replays its captured graphs
+    (one launch per graph instead of 229 kernel launches) and sleeps in the wait."""
     hm = S.make_model(S.QWEN25_1_5B, 20)
     toks = S.random_tokens(21, 2048, S.QWEN25_1_5B.vocab)
     dm = hip.DeviceModel(ctx, hm, 2048, 2048)
@@ -61,4 +63,4 @@ def test_prefill_call_cpu_share(ctx):
     wall, cpu = min(res)
     print(f"prefill call: wall {wall * 1e3:.2f} ms, engine-thread CPU {cpu * 1e3:.3f} ms "
           f"({100 * cpu / wall:.1f} %)")
-    assert cpu <= 0.2 * wall
+    assert cpu <= 0.05 * wall

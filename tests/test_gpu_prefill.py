@@ -7,6 +7,8 @@ Asserts mirror test_prefill.rs:829-885 (KV within one Q8_0 step, logits cosine,
 argmax) with the tighter bounds of this build: logits max rel err <= 1e-2 of the
 logit scale, top-1 agreement >= 99.5 % over all positions.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -191,6 +193,53 @@ def test_split_down_projection_runs_the_next_norm():
         assert kv_within_one_step(dk[l], okv.k[l], np.arange(104), dm.bpp)
         assert kv_within_one_step(dv[l], okv.v[l], np.arange(104), dm.bpp)
     dm.release()
+
+
+def _graph_sequence(ctx, hm, toks, cap, calls, reps):
+    """Runs the prefill calls (start_pos, n) in order `reps` times on one device model
+    and returns the logits and both rings after every call."""
+    dm = hip.DeviceModel(ctx, hm, cap, max(n for _, n in calls))
+    out = []
+    for rep in range(reps):
+        for pos, n in calls:
+            dm.embed(toks[pos:pos + n])
+            dm.execute_prefill_ubatch(pos, n)
+            dm.kv_sync_to_host(0, cap)
+            k, v = dm.kv_host()
+            out.append((dm.logits(), [a.copy() for a in k], [a.copy() for a in v]))
+            # eager work of the program's own between replays: a GEMM and a wait
+            hip.enqueue_gemm_q4_0_f16(ctx, dm.layers[0]["q"].scales, dm.layers[0]["q"].quants,
+                                      dm.scratch_bufs["h"], dm.scratch_bufs["q"], hm.cfg.q_dim, hm.cfg.embd, n)
+            ctx.wait()
+    dm.release()
+    return out
+
+
+@pytest.mark.parametrize("calls,cap", [([(0, 512)], 1024),                # prompt from position 0, kept window
+                                       ([(0, 512), (512, 256)], 1024),    # resume over the kept window
+                                       ([(0, 512), (512, 256)], 600)],    # the second ubatch wraps the ring
+                         ids=["fresh", "resume", "wrap"])
+def test_graph_replay_bit_identical(calls, cap):
+    """Graph replay (the default) against eager launches: the same sequence of prefill
+    calls, repeated three times with the program's own GEMM and wait between calls, gives
+    logits and K/V ring bytes identical to the same sequence run eagerly, after every
+    call (the first repetition captures each call's graphs, the others replay them)."""
+    cfg = dataclasses.replace(S.QWEN25_1_5B, n_layers=2, vocab=4096)
+    hm = S.make_model(cfg, 70, zero_mean=True)
+    toks = S.random_tokens(71, 768, cfg.vocab)
+    ctx = hip.HipContext.get_or_init(0)
+    try:
+        ctx.set_graph_replay(False)
+        eager = _graph_sequence(ctx, hm, toks, cap, calls, 3)
+        ctx.set_graph_replay(True)
+        replay = _graph_sequence(ctx, hm, toks, cap, calls, 3)
+    finally:
+        ctx.set_graph_replay(True)
+    for i, (lg, k, v) in enumerate(replay):
+        le, ke, ve = eager[i]
+        assert np.array_equal(lg.view(np.uint32), le.view(np.uint32)), f"logits of call {i}"
+        for l in range(cfg.n_layers):
+            assert np.array_equal(k[l], ke[l]) and np.array_equal(v[l], ve[l]), f"K/V of call {i}, layer {l}"
 
 
 def test_profiled_prefill_is_unchanged_and_counts_launches():

@@ -8,6 +8,8 @@ equal the allocating entry point's output bit for bit (same kernels, same plan),
 stay within the oracle's error bound. A matrix too large for the array is refused on
 the host.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -52,6 +54,59 @@ def test_noalloc_gemm_matches_allocating_entry_point(ctx):
     for _, _, bufs in ops.values():
         for b in bufs:
             b.release()
+
+
+def _free_device_bytes():
+    rt = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert rt.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_noalloc_gemm_allocates_nothing(ctx):
+    """The device's free memory is unchanged by two no-alloc calls on freshly uploaded
+    weights (24.8 MB in the GEMM layout, which the allocating entry point would build
+    and cache), and the allocating call that follows does lower it: the probe sees an
+    allocation of that size. Two contexts, each on its own stream, then call the entry
+    point back to back: the library orders them, and both outputs equal the allocating
+    entry point's."""
+    m_out, k, n_tok = 28672, 1536, 64
+    t, x, (sb, qb, xb) = _operands(ctx, 300, m_out, k, n_tok)
+    outs = [hip.HipBuffer.device_only(ctx, n_tok * m_out * 2) for _ in range(3)]
+    t2, x2, (sb2, qb2, xb2) = _operands(ctx, 310, 1536, 1536, 37)
+    o2 = hip.HipBuffer.device_only(ctx, 37 * 1536 * 2)
+    o2_ref = hip.HipBuffer.device_only(ctx, 37 * 1536 * 2)
+    # a first call loads the kernels' code objects (run alone, this test is their first user)
+    hip.enqueue_gemm_q4_0_f16_noalloc(ctx, sb2, qb2, xb2, o2, 1536, 1536, 37)
+    ctx.wait()
+    before = _free_device_bytes()
+    hip.enqueue_gemm_q4_0_f16_noalloc(ctx, sb, qb, xb, outs[0], m_out, k, n_tok)
+    hip.enqueue_gemm_q4_0_f16_noalloc(ctx, sb, qb, xb, outs[1], m_out, k, n_tok)
+    ctx.wait()
+    after = _free_device_bytes()
+    print(f"no-alloc: free device memory {before} -> {after} bytes", flush=True)
+    assert after == before
+    hip.enqueue_gemm_q4_0_f16(ctx, sb, qb, xb, outs[2], m_out, k, n_tok)
+    ctx.wait()
+    assert _free_device_bytes() < after
+    want = outs[2].download(np.uint16, (n_tok, m_out))
+    assert np.array_equal(outs[0].download(np.uint16, (n_tok, m_out)), want)
+    assert np.array_equal(outs[1].download(np.uint16, (n_tok, m_out)), want)
+    # two contexts (two streams) issuing no-alloc calls back to back
+    other = hip.HipContext.new(0)
+    try:
+        hip.enqueue_gemm_q4_0_f16_noalloc(ctx, sb, qb, xb, outs[0], m_out, k, n_tok)
+        hip.enqueue_gemm_q4_0_f16_noalloc(other, sb2, qb2, xb2, o2, 1536, 1536, 37)
+        other.wait()
+        ctx.wait()
+    finally:
+        other.release()
+    hip.enqueue_gemm_q4_0_f16(ctx, sb2, qb2, xb2, o2_ref, 1536, 1536, 37)
+    ctx.wait()
+    assert np.array_equal(outs[0].download(np.uint16, (n_tok, m_out)), want)
+    assert np.array_equal(o2.download(np.uint16, (37, 1536)), o2_ref.download(np.uint16, (37, 1536)))
+    for b in (sb, qb, xb, sb2, qb2, xb2, o2, o2_ref, *outs):
+        b.release()
 
 
 def test_noalloc_gemm_rejects_matrices_beyond_the_scratch(ctx):
