@@ -67,6 +67,9 @@ def parse():
     ap.add_argument("--cpu-sample", type=int, default=48, help="positions timed for the CPU baseline (0 = skip)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the per-shape GEMM table")
     ap.add_argument("--no-llama", action="store_true", help="skip the Llama-3.2-3B 4 x 4096 prefill rate")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch every kernel one by one instead of replaying captured HIP graphs (for tools "
+                         "that trace kernel dispatches)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB three times (the known-size "
                          "reference for FETCH_SIZE/WRITE_SIZE counter passes) and exit")
@@ -229,6 +232,7 @@ def main():
     cfg = S.QWEN25_1_5B
     T = a.prompt
     ctx = hip.HipContext.get_or_init(0)
+    ctx.set_graph_replay(not a.no_graph)
     hm = S.make_model(cfg, SEED_MODEL)
     tokens = S.random_tokens(SEED_TOKENS, T, cfg.vocab)
     dm = hip.DeviceModel(ctx, hm, capacity=T, max_n=min(a.ubatch, T))
@@ -275,7 +279,7 @@ def main():
     for _ in range(a.warmup):
         step()
     wall_eager = timed_steps()
-    ctx.set_graph_replay(True)
+    ctx.set_graph_replay(not a.no_graph)
 
     # Kernel timing: the same K steps again with a hipEvent pair per launch on the
     # library's stream. The GEMM kernels stamp their pair with their own start and end
