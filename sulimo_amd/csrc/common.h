@@ -211,10 +211,13 @@ struct GemmArgs {
   int nseg;
   // K split across workgroups (EPI_PART only): `splits` workgroups per tile, split s
   // covering k stages [s * split_stages, (s + 1) * split_stages) of 64, each writing its
-  // partial sums to part + s * m * ldp, column = (columns of the segments before) + col.
+  // partial sums to element s * m * ldp + row * ldp + column of part (column = columns
+  // of the segments before + col). part_f16: the partials are stored as f16 (for a
+  // GEMM whose output is rounded to f16 anyway), else f32.
   int splits, split_stages;
   float *part;
   int ldp;
+  int part_f16;
   // Workspace launch_gemm_q4_0 may use for K-split partials (none when part is null).
   size_t part_bytes;
   // Tile grid, filled by the launcher: tiles_m x tiles_n tiles, visited in groups of
@@ -236,8 +239,9 @@ struct GemmArgs {
 };
 
 // Runs X W^T with the tile configuration and K split a cost model picks for the shape;
-// a K split writes f32 partials to a.part (a.part_bytes) and reduces them in a second
-// kernel. With a.norm_w set and norm_done given, *norm_done tells whether that
+// a K split writes partials to a.part (a.part_bytes), f16 when the output is f16 (the
+// f16 and residual epilogues) and f32 for an f32 output, and reduces them in f32 in a
+// second kernel. With a.norm_w set and norm_done given, *norm_done tells whether that
 // reduction also produced the RMSNorm of the updated rows.
 // A non-null stamp takes the start of the first kernel and the end of the last.
 int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done = nullptr,

@@ -155,6 +155,17 @@ __device__ __forceinline__ float4 quad_t32(float a0, float a1, float a2, float a
   const float t0 = uf(dpp_xor2(fu(h ? x0 : y0))), t1 = uf(dpp_xor2(fu(h ? x1 : y1)));
   return h ? float4{t0, t1, y0, y1} : float4{x0, x1, t0, t1};
 }
+// Four consecutive K-split partials as f32, stored as f16 or f32.
+template <bool F16>
+__device__ __forceinline__ float4 load_part4(const float *part, size_t idx) {
+  if constexpr (F16) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 v = *reinterpret_cast<const h4 *>(reinterpret_cast<const _Float16 *>(part) + idx);
+    return float4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+  } else {
+    return *reinterpret_cast<const float4 *>(part + idx);
+  }
+}
 __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
 }
@@ -931,8 +942,20 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
               float *dst;
               bool vec;
               if constexpr (EPI == EPI_PART) {
-                dst = a.part + (size_t)ks * a.m * a.ldp + colbase + (size_t)row * a.ldp + col;
-                vec = col + 4 <= seg.n;  // partial planes are 4-column aligned
+                const size_t pi = (size_t)ks * a.m * a.ldp + colbase + (size_t)row * a.ldp + col;
+                if (a.part_f16) {  // partials of an f16 output: one f16 rounding each
+                  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                  _Float16 *pd = reinterpret_cast<_Float16 *>(a.part) + pi;
+                  if (col + 4 <= seg.n) {  // partial planes are 4-column aligned
+                    *reinterpret_cast<h4 *>(pd) = h4{(_Float16)o.x, (_Float16)o.y, (_Float16)o.z, (_Float16)o.w};
+                  } else {
+                    const float w[4] = {o.x, o.y, o.z, o.w};
+                    for (int e = 0; e < 4 && col + e < seg.n; e++) pd[e] = (_Float16)w[e];
+                  }
+                  continue;
+                }
+                dst = a.part + pi;
+                vec = col + 4 <= seg.n;
               } else {
                 dst = reinterpret_cast<float *>(seg.out) + (size_t)row * seg.ldo + seg.col0 + col;
                 vec = vec_ok && col + 4 <= seg.n;
@@ -965,16 +988,17 @@ __global__ __launch_bounds__(256 * KSPLIT, (WM == 2 || KSPLIT > 1) ? 1 : 2) void
 // one thread per 4 consecutive columns of the concatenated segment columns of a row.
 template <int EPI>
 __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs a) {
+  constexpr bool kF16 = EPI != EPI_F32;  // partials at the output's precision
   const int c4 = a.ldp / 4;
   const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (long)a.m * c4) return;
   const int row = (int)(gid / c4);
   int col = (int)(gid - (long)row * c4) * 4;
   const size_t plane = (size_t)a.m * a.ldp;
-  const float *p = a.part + (size_t)row * a.ldp + col;
-  float4 v = *reinterpret_cast<const float4 *>(p);
+  const size_t p = (size_t)row * a.ldp + col;
+  float4 v = load_part4<kF16>(a.part, p);
   for (int s = 1; s < a.splits; s++) {
-    const float4 w = *reinterpret_cast<const float4 *>(p + s * plane);
+    const float4 w = load_part4<kF16>(a.part, p + s * plane);
     v.x += w.x;
     v.y += w.y;
     v.z += w.z;
@@ -1017,7 +1041,7 @@ __global__ __launch_bounds__(256) void split_reduce_norm_vec_kernel(GemmArgs a) 
   if (row >= a.m) return;
   const GemmSegment seg = a.seg[0];
   const size_t plane = (size_t)a.m * a.ldp;
-  const float *p = a.part + (size_t)row * a.ldp;
+  const size_t p = (size_t)row * a.ldp;  // f16 partials (a residual GEMM's output is f16)
   float *x = reinterpret_cast<float *>(seg.out) + (size_t)row * seg.ldo;
   // every load before the first store (loads and stores retire in issue order)
   float4 v[V], nw[V], old[V];
@@ -1025,13 +1049,13 @@ __global__ __launch_bounds__(256) void split_reduce_norm_vec_kernel(GemmArgs a) 
   for (int j = 0; j < V; j++) {
     const int c = 256 * j + 4 * lane;
     nw[j] = *reinterpret_cast<const float4 *>(a.norm_w + c);
-    v[j] = *reinterpret_cast<const float4 *>(p + c);
+    v[j] = load_part4<true>(a.part, p + c);
     old[j] = *reinterpret_cast<const float4 *>(x + c);
   }
   for (int sp = 1; sp < a.splits; sp++) {
     float4 w[V];
 #pragma unroll
-    for (int j = 0; j < V; j++) w[j] = *reinterpret_cast<const float4 *>(p + sp * plane + 256 * j + 4 * lane);
+    for (int j = 0; j < V; j++) w[j] = load_part4<true>(a.part, p + sp * plane + 256 * j + 4 * lane);
 #pragma unroll
     for (int j = 0; j < V; j++) {
       v[j].x += w[j].x;
@@ -1087,7 +1111,7 @@ __global__ __launch_bounds__(256) void split_reduce_norm_kernel(GemmArgs a) {
   const GemmSegment seg = a.seg[0];
   const int n4 = seg.n / 4;
   const size_t plane = (size_t)a.m * a.ldp;
-  const float *p = a.part + (size_t)row * a.ldp;
+  const size_t p = (size_t)row * a.ldp;  // f16 partials (a residual GEMM's output is f16)
   float *x = reinterpret_cast<float *>(seg.out) + (size_t)row * seg.ldo;
   // the norm weights are loaded first: loaded between the stores at the end, each load
   // would wait for the stores before it (loads and stores retire in issue order)
@@ -1100,9 +1124,9 @@ __global__ __launch_bounds__(256) void split_reduce_norm_kernel(GemmArgs a) {
     const int c4 = tid + 256 * j;
     xv[j] = float4{0.0f, 0.0f, 0.0f, 0.0f};
     if (c4 >= n4) continue;
-    float4 v = *reinterpret_cast<const float4 *>(p + 4 * c4);
+    float4 v = load_part4<true>(a.part, p + 4 * c4);
     for (int sp = 1; sp < a.splits; sp++) {
-      const float4 w = *reinterpret_cast<const float4 *>(p + sp * plane + 4 * c4);
+      const float4 w = load_part4<true>(a.part, p + sp * plane + 4 * c4);
       v.x += w.x;
       v.y += w.y;
       v.z += w.z;
@@ -1400,6 +1424,9 @@ int seg_cols(const GemmArgs &a) {
   return n;
 }
 
+// Bytes per stored K-split partial: f16 for f16-rounded outputs, f32 for an f32 output.
+int part_elem_bytes(const GemmArgs &a) { return a.epi == EPI_F32 ? 4 : 2; }
+
 double predict_us(const GemmArgs &a, int cfg, int splits, int cus) {
   int per;
   splits = normalize_splits(a.k, splits, &per);
@@ -1416,7 +1443,7 @@ double predict_us(const GemmArgs &a, int cfg, int splits, int cus) {
   if (splits > 1) {
     const double mn = (double)a.m * seg_cols(a);
     const double out_bytes = a.epi == EPI_RESID ? 8 : a.epi == EPI_F32 ? 4 : 2;
-    t += kReduceFixed + kReducePerMB * (splits * mn * 4 + mn * out_bytes) / 1e6;
+    t += kReduceFixed + kReducePerMB * (splits * mn * part_elem_bytes(a) + mn * out_bytes) / 1e6;
   }
   return t;
 }
@@ -1428,7 +1455,7 @@ bool can_split(const GemmArgs &a, int splits, bool unbounded) {
   for (int i = 0; i < a.nseg; i++)
     if (a.seg[i].n % 4 || a.seg[i].ldo % 4 || a.seg[i].col0 % 4) return false;
   if (unbounded) return true;
-  return a.part && (size_t)splits * a.m * seg_cols(a) * 4 <= a.part_bytes;
+  return a.part && (size_t)splits * a.m * seg_cols(a) * part_elem_bytes(a) <= a.part_bytes;
 }
 
 // The RoPE epilogue runs on 128-column tiles (one wave per 32 columns: its cos/sin,
@@ -1515,7 +1542,7 @@ size_t gemm_q4_0_workspace_bytes(const GemmArgs &a) {
   if (a.m <= 0 || a.k <= 0 || a.k % 32 != 0 || a.nseg < 1 || a.nseg > 3) return 0;
   if (gemv_fits(a)) return 0;
   const GemmPlan p = plan_gemm(a, true);
-  return p.splits > 1 ? (size_t)p.splits * a.m * seg_cols(a) * 4 : 0;
+  return p.splits > 1 ? (size_t)p.splits * a.m * seg_cols(a) * part_elem_bytes(a) : 0;
 }
 
 int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done, const LaunchStamp *stamp) {
@@ -1557,11 +1584,12 @@ int32_t launch_gemm_q4_0(const GemmArgs &a, hipStream_t s, bool *norm_done, cons
   if (gemv_fits(a)) return launch_gemv(a, s, st);
   const GemmPlan p = plan_gemm(a, false);
   if (p.splits == 1) return launch_plan(a, p.cfg, s, st);
-  // K split: f32 partials per split, then their sum in split order with the epilogue
+  // K split: partials per split, then their sum in split order with the epilogue
   GemmArgs g = a;
   g.epi = EPI_PART;
   g.splits = p.splits;
   g.ldp = seg_cols(a);
+  g.part_f16 = part_elem_bytes(a) == 2;
   int32_t rc = launch_plan(g, p.cfg, s, LaunchStamp{st.start, nullptr});
   if (rc) return rc;
   GemmArgs r = g;
