@@ -381,6 +381,11 @@ int32_t sulimo_hip_set_profiling(sulimo_hip_ctx *ctx, int32_t enable);
  * with per-position outputs run eagerly. Results are bit-identical either way.
  * Disabling it also frees the cached graphs. */
 int32_t sulimo_hip_set_graph_replay(sulimo_hip_ctx *ctx, int32_t enable);
+/* Backend tuning switch (no counterpart in the reference). When the attention splits a
+ * query block's keys over several workgroups, the last workgroup to finish a block
+ * merges its pieces (default), or with enable != 0 a separate kernel launch merges them.
+ * Results are bit-identical either way. */
+int32_t sulimo_hip_set_attention_merge_kernel(sulimo_hip_ctx *ctx, int32_t enable);
 int32_t sulimo_hip_get_prefill_stats(const sulimo_hip_ctx *ctx, sulimo_hip_prefill_stats *out);
 
 /* Record a start event on the context stream; stop records the end event, waits for

@@ -33,8 +33,13 @@
 //     into pieces of at most C steps (C from a cost model of the workgroups, which
 //     also favours splitting few long blocks over many CUs): every workgroup runs
 //     one piece, heaviest blocks first. A block in one piece writes
-//     its f16 output; the pieces of a split block write (O, m, l) partials, and
-//  3. attn_merge_kernel combines them (the same rescale-and-add as the halves).
+//     its f16 output; the pieces of a split block write (O, m, l) partials with
+//     device-scope stores and count in on a per-(block, query wave) counter; the wave
+//     that completes the count combines the pieces in piece order (the same
+//     rescale-and-add as the halves). Device-scope (sc1) stores and loads stay
+//     coherent across the XCDs' L2 caches, so no cache writeback fence is needed.
+//  3. attn_merge_kernel does that combination instead, as a separate launch, when
+//     the caller passes no counters.
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
@@ -76,6 +81,63 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 __device__ __forceinline__ void wait_vmcnt0() { wait_vmcnt<0>(); }
+
+// Device-scope (sc1) stores and loads: coherent across the XCDs' L2 caches by
+// themselves, for the partials one workgroup hands to another within a launch.
+__device__ __forceinline__ void st_dev(half4 *p, half4 v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t *>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(float *p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t *>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ half4 ld_dev(const half4 *p) {
+  return __builtin_bit_cast(half4, __hip_atomic_load(reinterpret_cast<uint64_t *>(const_cast<half4 *>(p)),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+  return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<uint32_t *>(const_cast<float *>(p)),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// f16(v * s) for four values: the f32 product, then its f16 rounding. Kept from fusing
+// into one rounding (v_fma_mix), so that every path storing an output row or a piece's
+// record rounds the same way.
+__device__ __forceinline__ half4 scale_h4(float a, float b, float c, float d, float s) {
+  float x = a * s, y = b * s, z = c * s, w = d * s;
+  asm("" : "+v"(x), "+v"(y), "+v"(z), "+v"(w));
+  return half4{(_Float16)x, (_Float16)y, (_Float16)z, (_Float16)w};
+}
+
+// Combination of a split block's pieces in piece order: piece p's normalized f16 output
+// counts with weight l_p * 2^(m_p - max m) (m in log2 units, l its row sum); the result
+// is the weighted sum over the summed weights.
+template <int NV>
+struct PieceMerge {
+  float ms, l, o[NV];
+  __device__ __forceinline__ explicit PieceMerge(float mmax) : ms(mmax == -INFINITY ? 0.0f : mmax), l(0.0f) {
+#pragma unroll
+    for (int r = 0; r < NV; r++) o[r] = 0.0f;
+  }
+  __device__ __forceinline__ void add(float mp, float lp, const half4 *v) {
+    // no contraction: l += w must not become fma(lp, 2^.., l) at one call site and not
+    // at another (the in-kernel merge takes its own piece from registers, the others
+    // from memory, and must give the same bits whichever piece finishes last)
+#pragma clang fp contract(off)
+    const float w = lp * __builtin_amdgcn_exp2f(mp - ms);
+    l += w;
+#pragma unroll
+    for (int r = 0; r < NV; r++) o[r] = __builtin_fmaf((float)v[r >> 2][r & 3], w, o[r]);
+  }
+  __device__ __forceinline__ float inv() const { return l > 0.0f ? 1.0f / l : 0.0f; }
+};
+
+// 4 query waves = HG query heads of one KV group x PB blocks of 32 positions.
+__host__ __device__ inline void query_wave_layout(int G, int *HG, int *PB) {
+  *HG = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
+  *PB = 4 / *HG;
+}
 
 // Key steps of query block qblk (64-key tiles, one per half and step).
 __host__ __device__ inline int attn_block_steps(int qblk, int PB, int n, int start_pos, int cap, int wlo,
@@ -172,7 +234,7 @@ constexpr int part_rec_floats() { return 16 * (HD / 32) * 128 + 2 * 256; }
 template <int HD, int H2>
 __global__ __launch_bounds__(256 * H2, 2 / H2) void flash_attn_kernel(AttnArgs a, long wlo, int wpad, int HG,
                                                                       int PB, int n_qblk, int n_hgrp, int C,
-                                                                      float *part, int pmax) {
+                                                                      float *part, int pmax, int *ctr) {
   constexpr int KS = HD / 16;          // S^T k-steps over head_dim
   constexpr int OT = HD / 32;          // O^T tiles over head_dim
   constexpr int KCH = HD / 8;          // 16-byte chunks per K row
@@ -457,18 +519,90 @@ __global__ __launch_bounds__(256 * H2, 2 / H2) void flash_attn_kernel(AttnArgs a
 
   if (npiece > 1) {  // a piece of a split block: its partial (O^T, m, l) for the merge
     constexpr int RF = part_rec_floats<HD>();
-    float *rec = part + (((size_t)grp * n_qblk + qblk) * pmax + piece) * (size_t)RF;
+    constexpr int MOFF = 16 * OT * 128;  // m, then l, after the O^T groups
+    float *rec0 = part + ((size_t)grp * n_qblk + qblk) * pmax * (size_t)RF;
+    float *rec = rec0 + (size_t)piece * RF;
     const float lt = lrun + __shfl_xor(lrun, 32, 64);  // the query's l (lane halves hold parts)
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    half4 *ro = reinterpret_cast<half4 *>(rec) + ci;
+    half4 mine[4 * OT];
 #pragma unroll
     for (int i = 0; i < OT; i++)
 #pragma unroll
       for (int g = 0; g < 4; g++)
-        ro[(4 * i + g) * 256] = half4{(_Float16)(o[i][4 * g] * inv), (_Float16)(o[i][4 * g + 1] * inv),
-                                      (_Float16)(o[i][4 * g + 2] * inv), (_Float16)(o[i][4 * g + 3] * inv)};
-    rec[16 * OT * 128 + ci] = mrun;
-    rec[16 * OT * 128 + 256 + ci] = lt;
+        mine[4 * i + g] = scale_h4(o[i][4 * g], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3], inv);
+    half4 *ro = reinterpret_cast<half4 *>(rec) + ci;
+#pragma unroll
+    for (int k = 0; k < 4 * OT; k++) {
+      // one materialization: the merge below uses exactly the stored f16 values
+      uint64_t u = __builtin_bit_cast(uint64_t, mine[k]);
+      asm volatile("" : "+v"(u));
+      mine[k] = __builtin_bit_cast(half4, u);
+      st_dev(ro + k * 256, mine[k]);
+    }
+    st_dev(rec + MOFF + ci, mrun);
+    st_dev(rec + MOFF + 256 + ci, lt);
+    if (!ctr || !wave_live) return;  // a wave past the last token is past it in every piece
+    // Count in once this wave's record is complete (device-scope stores, acknowledged);
+    // the wave that completes the count merges the pieces for its 32 queries and
+    // leaves the counter at zero for the next launch.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int *cw = ctr + (((size_t)grp * n_qblk + qblk) << 2) + qw;
+    int prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(cw, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev != npiece - 1) return;
+    if (lane == 0) __hip_atomic_store(cw, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // piece p's (O, m, l): this piece's from registers, the others' loaded (issued
+    // one piece ahead of their use, so two pieces' loads are in flight at a time)
+    auto fetch = [&](int p, half4 (&v)[4 * OT], float &mp, float &lp) __attribute__((always_inline)) {
+      if (p == piece) {
+#pragma unroll
+        for (int k = 0; k < 4 * OT; k++) v[k] = mine[k];
+        mp = mrun;
+        lp = lt;
+        return;
+      }
+      const float *r = rec0 + (size_t)p * RF;
+      const half4 *rv = reinterpret_cast<const half4 *>(r) + ci;
+#pragma unroll
+      for (int k = 0; k < 4 * OT; k++) v[k] = ld_dev(rv + k * 256);
+      mp = ld_dev(r + MOFF + ci);
+      lp = ld_dev(r + MOFF + 256 + ci);
+    };
+    half4 va[4 * OT], vb[4 * OT];
+    float ma, la, mb = 0.0f, lb = 0.0f;
+    fetch(0, va, ma, la);
+    if (npiece > 1) fetch(1, vb, mb, lb);
+    float mmax = -INFINITY;
+    for (int p0 = 0; p0 < npiece; p0 += 8) {  // loads of 8 pieces issued before any is used
+      float mp[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int p = p0 + j;
+        mp[j] = p >= npiece ? -INFINITY : p == piece ? mrun : ld_dev(rec0 + (size_t)p * RF + MOFF + ci);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; j++) mmax = fmaxf(mmax, mp[j]);
+    }
+    PieceMerge<16 * OT> mg(mmax);
+    int p = 0;
+    for (; p + 1 < npiece; p += 2) {
+      mg.add(ma, la, va);
+      if (p + 2 < npiece) fetch(p + 2, va, ma, la);
+      mg.add(mb, lb, vb);
+      if (p + 3 < npiece) fetch(p + 3, vb, mb, lb);
+    }
+    if (p < npiece) mg.add(ma, la, va);
+    if (t >= a.n) return;
+    const float minv = mg.inv();
+    _Float16 *dst = reinterpret_cast<_Float16 *>(a.out) + (size_t)t * qd + (size_t)h * HD;
+#pragma unroll
+    for (int i = 0; i < OT; i++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const float *w = mg.o + 16 * i + 4 * g;
+        *reinterpret_cast<half4 *>(dst + 32 * i + 8 * g + 4 * lg) = scale_h4(w[0], w[1], w[2], w[3], minv);
+      }
     return;
   }
 
@@ -481,9 +615,8 @@ __global__ __launch_bounds__(256 * H2, 2 / H2) void flash_attn_kernel(AttnArgs a
   for (int i = 0; i < OT; i++)
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-      const half4 v = {(_Float16)(o[i][4 * g] * inv), (_Float16)(o[i][4 * g + 1] * inv),
-                       (_Float16)(o[i][4 * g + 2] * inv), (_Float16)(o[i][4 * g + 3] * inv)};
-      *reinterpret_cast<half4 *>(dst + 32 * i + 8 * g + 4 * lg) = v;
+      *reinterpret_cast<half4 *>(dst + 32 * i + 8 * g + 4 * lg) =
+          scale_h4(o[i][4 * g], o[i][4 * g + 1], o[i][4 * g + 2], o[i][4 * g + 3], inv);
     }
 }
 
@@ -509,50 +642,33 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a, long wlo, i
   const int h = kvh * G + hgrp * HG + hj;
   const int t = (qblk * PB + pb) * 32 + (lane & 31);
   const int lg = lane >> 5;
+  constexpr int MOFF = 16 * OT * 128;
   const float *rec0 = part + ((size_t)grp * n_qblk + qblk) * pmax * (size_t)RF;
-  // every load of a piece is issued before any is used; piece p contributes its
-  // normalized O with weight l_p * 2^(m_p - m)
-  float m = -INFINITY, l = 0.0f, o[16];
-#pragma unroll
-  for (int r = 0; r < 16; r++) o[r] = 0.0f;
+  // the block's max first (the loads of PMAX pieces issued before any is used)
+  float mmax = -INFINITY;
   for (int p0 = 0; p0 < npiece; p0 += PMAX) {
-    const int np = min(PMAX, npiece - p0);
     float mp[PMAX];
 #pragma unroll
-    for (int p = 0; p < PMAX; p++) mp[p] = p < np ? rec0[(size_t)(p0 + p) * RF + 16 * OT * 128 + ci] : -INFINITY;
-    float mm = m;
+    for (int p = 0; p < PMAX; p++) mp[p] = p0 + p < npiece ? rec0[(size_t)(p0 + p) * RF + MOFF + ci] : -INFINITY;
 #pragma unroll
-    for (int p = 0; p < PMAX; p++) mm = fmaxf(mm, mp[p]);
-    const float ms = mm == -INFINITY ? 0.0f : mm;
-    const float a0 = __builtin_amdgcn_exp2f(m - ms);
-    l *= a0;
+    for (int p = 0; p < PMAX; p++) mmax = fmaxf(mmax, mp[p]);
+  }
+  PieceMerge<16> mg(mmax);
+  for (int p = 0; p < npiece; p++) {
+    const float *rec = rec0 + (size_t)p * RF;
+    const half4 *ro = reinterpret_cast<const half4 *>(rec) + ci;
+    half4 v[4];
 #pragma unroll
-    for (int r = 0; r < 16; r++) o[r] *= a0;
-    m = mm;
-    for (int p = 0; p < np; p++) {
-      const float *rec = rec0 + (size_t)(p0 + p) * RF;
-      const half4 *ro = reinterpret_cast<const half4 *>(rec) + ci;
-      float v[16];
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const half4 hv = ro[(4 * i + g) * 256];
-#pragma unroll
-        for (int e = 0; e < 4; e++) v[4 * g + e] = (float)hv[e];
-      }
-      const float w = rec[16 * OT * 128 + 256 + ci] * __builtin_amdgcn_exp2f(mp[p] - ms);
-      l += w;
-#pragma unroll
-      for (int r = 0; r < 16; r++) o[r] += v[r] * w;
-    }
+    for (int g = 0; g < 4; g++) v[g] = ro[(4 * i + g) * 256];
+    mg.add(rec[MOFF + ci], rec[MOFF + 256 + ci], v);
   }
   if (t >= a.n) return;
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  const float inv = mg.inv();
   _Float16 *dst = reinterpret_cast<_Float16 *>(a.out) + (size_t)t * a.n_head * HD + (size_t)h * HD;
 #pragma unroll
   for (int g = 0; g < 4; g++) {
-    const half4 v = {(_Float16)(o[4 * g] * inv), (_Float16)(o[4 * g + 1] * inv), (_Float16)(o[4 * g + 2] * inv),
-                     (_Float16)(o[4 * g + 3] * inv)};
-    *reinterpret_cast<half4 *>(dst + 32 * i + 8 * g + 4 * lg) = v;
+    const float *w = mg.o + 4 * g;
+    *reinterpret_cast<half4 *>(dst + 32 * i + 8 * g + 4 * lg) = scale_h4(w[0], w[1], w[2], w[3], inv);
   }
 }
 
@@ -562,19 +678,17 @@ struct AttnPlan {
   int halves;                                   // key halves inside a workgroup (1 or 2)
 };
 
-// Predicted time (us) of one layout, from workgroup costs measured on MI355X at
-// head_dim 128 (clock ramped; half the step cost at 64). Two key halves per
-// workgroup: one workgroup per CU, ~11.5 us fixed (Q load, first K/V tiles, merge of
-// the halves) + ~1.85 us per step of two tiles. One half: two workgroups per CU,
-// ~17 us fixed + ~0.9 us per tile. A split adds the merge kernel (~3 us plus its
-// partial traffic, written and read at cache rate).
+// Predicted time (us) of one layout, fitted to the measured time of every layout and
+// piece size on MI355X over 17 shapes (Qwen2.5-1.5B, Llama-3.2-3B and a head_dim-64
+// model; prompts of 7 to 4096 tokens at several start positions): the workgroups run in
+// rounds of one per slot (two per CU with one key half, one with two), each round as
+// long as a piece of C steps, fixed + per-step cost; a split block adds ~1 us per piece
+// of the longest split (its last wave merges the pieces).
 AttnPlan plan_layout(const AttnArgs &a, const Window &w, int halves, int force_c, double *t_out) {
   AttnPlan p;
   p.halves = halves;
-  // 4 query waves = HG heads of one KV group x PB blocks of 32 positions
   const int G = a.n_head / a.n_head_kv;
-  p.HG = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
-  p.PB = 4 / p.HG;
+  query_wave_layout(G, &p.HG, &p.PB);
   p.n_qblk = (a.n + 32 * p.PB - 1) / (32 * p.PB);
   p.n_hgrp = G / p.HG;
   const int n_groups = a.n_head_kv * p.n_hgrp;
@@ -582,22 +696,21 @@ AttnPlan plan_layout(const AttnArgs &a, const Window &w, int halves, int force_c
   for (int b = 0; b < p.n_qblk; b++)
     maxs = std::max(maxs, attn_block_steps(b, p.PB, a.n, a.start_pos, a.capacity, (int)w.lo, halves));
   const double slots = (double)device_cu_count() * (halves == 2 ? 1 : 2);
-  const double hs = a.head_dim > 64 ? 1.0 : 0.5;
-  const double f = halves == 2 ? 11.5 : 17.0, g = (halves == 2 ? 1.85 : 0.9) * hs;
-  const double rec_bytes = (16.0 * (a.head_dim / 32) * 128 + 512) * 4;
+  const bool hd64 = a.head_dim <= 64;
+  const double f = (halves == 2 ? 11.515 : 7.482) * (hd64 ? 1.181 : 1.0);
+  const double g = (halves == 2 ? 1.101 : 1.55) * (hd64 ? 0.473 : 1.0);
   auto cost = [&](int C, int *pieces, int *pmax) {
-    int np = 0, pm = 1, split_pieces = 0;
+    int np = 0, pm = 1;
     for (int b = 0; b < p.n_qblk; b++) {
       const int k = attn_pieces(attn_block_steps(b, p.PB, a.n, a.start_pos, a.capacity, (int)w.lo, halves), C);
       np += k;
       pm = std::max(pm, k);
-      if (k > 1) split_pieces += k;
     }
     *pieces = np;
     *pmax = pm;
     const double rounds = std::ceil((double)np * n_groups / slots);
     double t = rounds * (f + g * std::min(C, maxs));
-    if (pm > 1) t += 3.0 + (double)split_pieces * n_groups * rec_bytes * 2 / 10e12 * 1e6;
+    if (pm > 1) t += 1.017 * pm;
     return t;
   };
   if (force_c > 0) {
@@ -610,7 +723,7 @@ AttnPlan plan_layout(const AttnArgs &a, const Window &w, int halves, int force_c
   for (int C = 2; C < maxs; C++) {
     int np, pm;
     const double t = cost(C, &np, &pm);
-    if (t < best * 0.97) {  // split only for a clear gain
+    if (t < best) {
       best = t;
       p.C = C;
       p.pieces = np;
@@ -694,15 +807,19 @@ int32_t launch_hd(const AttnArgs &a, hipStream_t s) {
   const AttnPlan p = plan_attention(a, w);
   float *part = a.part ? a.part : reinterpret_cast<float *>(reinterpret_cast<char *>(a.window) + window_bytes(a, w));
   const int n_groups = a.n_head_kv * p.n_hgrp;
+  // the pieces of split blocks merge themselves when the caller passes counters
+  int *ctr = p.pmax >= 2 ? a.ctr : nullptr;
+  if (ctr && a.ctr_ints < (size_t)n_groups * p.n_qblk * 4)
+    return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "attention counters too small for the call");
   if (p.halves == 2)
     hipLaunchKernelGGL((flash_attn_kernel<HD, 2>), dim3(p.pieces * n_groups), dim3(512), 0, s, a, w.lo, w.pad, p.HG,
-                       p.PB, p.n_qblk, p.n_hgrp, p.C, part, p.pmax);
+                       p.PB, p.n_qblk, p.n_hgrp, p.C, part, p.pmax, ctr);
   else
     hipLaunchKernelGGL((flash_attn_kernel<HD, 1>), dim3(p.pieces * n_groups), dim3(256), 0, s, a, w.lo, w.pad, p.HG,
-                       p.PB, p.n_qblk, p.n_hgrp, p.C, part, p.pmax);
+                       p.PB, p.n_qblk, p.n_hgrp, p.C, part, p.pmax, ctr);
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "flash_attn_kernel launch");
-  if (p.pmax < 2) return SULIMO_HIP_OK;
+  if (p.pmax < 2 || ctr) return SULIMO_HIP_OK;
   hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(p.n_qblk, n_groups, HD / 32), dim3(256), 0, s, a, w.lo, p.HG, p.PB,
                      p.n_qblk, p.n_hgrp, p.C, part, p.pmax, p.halves);
   e = hipGetLastError();
@@ -717,6 +834,14 @@ AttnWindowLayout attention_window_layout(const AttnArgs &a) {
 }
 
 size_t attention_window_bytes(const AttnArgs &a) { return window_bytes(a, window_of(a)); }
+
+size_t attention_counter_ints(const AttnArgs &a) {
+  if (a.n <= 0 || a.n_head_kv <= 0 || a.n_head % a.n_head_kv != 0) return 0;
+  const int G = a.n_head / a.n_head_kv;
+  int HG, PB;
+  query_wave_layout(G, &HG, &PB);
+  return (size_t)a.n_head_kv * (G / HG) * ((a.n + 32 * PB - 1) / (32 * PB)) * 4;
+}
 
 size_t attention_workspace_bytes(const AttnArgs &a) {
   if (a.n <= 0 || a.n_head_kv <= 0 || a.n_head % a.n_head_kv != 0 || a.capacity <= 0) return 0;

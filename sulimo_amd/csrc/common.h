@@ -77,6 +77,12 @@ struct sulimo_hip_ctx {
   sulimo_hip_prefill_stats stats{};
   // Graph replay of execute_prefill_ubatch (sulimo_hip_set_graph_replay).
   bool graph_replay = true;
+  // Arrival counters of split attention blocks (AttnArgs::ctr; zero between calls),
+  // and whether a separate kernel merges the pieces instead
+  // (sulimo_hip_set_attention_merge_kernel).
+  int *attn_ctr = nullptr;
+  size_t attn_ctr_n = 0;
+  bool attn_merge_kernel = false;
   std::vector<PrefillGraph> graphs;
   uint64_t graph_tick = 0;
 };
@@ -124,6 +130,10 @@ int32_t fail(int32_t code, const std::string &msg);
 int32_t hip_fail(hipError_t e, const char *what);
 // Grows ctx->ws to at least `bytes` (synchronizes the stream before freeing the old one).
 int32_t ensure_workspace(sulimo_hip_ctx *ctx, size_t bytes);
+// Grows ctx->attn_ctr to at least n zeroed ints (on the context stream; not while a
+// graph is being captured). *out: the counters, or null when the separate merge kernel
+// is selected.
+int32_t ensure_attn_counters(sulimo_hip_ctx *ctx, size_t n, int **out);
 // Events a launch stamps with its kernels' own start and end times (hipExtLaunchKernel):
 // the interval between them leaves out the dispatch gap that an event recorded on the
 // stream ahead of the launch adds. Both null: an ordinary launch.
@@ -374,10 +384,17 @@ struct AttnArgs {
   // mask removes. part is then where the split-key partials go (else after the window).
   int win_pad, win_valid;
   float *part;
+  // ctr_ints (at least attention_counter_ints) zero-initialized ints, or null. When
+  // set, the last wave to finish a split block's queries merges the block's pieces
+  // itself (and resets its counter to zero); when null, a separate kernel merges them.
+  int *ctr;
+  size_t ctr_ints;
 };
 // Device bytes of AttnArgs::window for this attention call (depends on the shapes and
 // on the device's compute-unit count).
 size_t attention_workspace_bytes(const AttnArgs &a);
+// Arrival counters AttnArgs::ctr must hold for this call's shape.
+size_t attention_counter_ints(const AttnArgs &a);
 int32_t launch_attention(const AttnArgs &a, hipStream_t s);
 
 // The f16 key window of an attention call: window index j holds position lo + j for

@@ -285,6 +285,8 @@ int32_t sulimo_hip_enqueue_attention_prefill(sulimo_hip_ctx *ctx, const sulimo_h
   a.head_dim = (int)head_dim;
   if ((rc = ensure_workspace(ctx, attention_workspace_bytes(a)))) return rc;
   a.window = ctx->ws;
+  a.ctr_ints = attention_counter_ints(a);
+  if ((rc = ensure_attn_counters(ctx, a.ctr_ints, &a.ctr))) return rc;
   wrote(out);
   return launch_attention(a, ctx->stream);
 }
@@ -579,6 +581,9 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
   }
   const size_t ws_need = off_g + gemm_ws;
   if ((rc = ensure_workspace(ctx, ws_need))) return rc;
+  int *attn_ctr = nullptr;
+  const size_t attn_ctr_ints = attention_counter_ints(probe_at);
+  if ((rc = ensure_attn_counters(ctx, attn_ctr_ints, &attn_ctr))) return rc;
   char *ws = reinterpret_cast<char *>(ctx->ws);
   float *xres = reinterpret_cast<float *>(ws);
   float *gemm_part = reinterpret_cast<float *>(ws + off_g);
@@ -699,6 +704,8 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     at.n_head_kv = (int)Hkv;
     at.head_dim = (int)hd;
     at.window = ws + off_w;
+    at.ctr = attn_ctr;
+    at.ctr_ints = attn_ctr_ints;
     if (keep_win) {
       at.win_pad = kv->k_buffers[l]->kvwin.pad;
       at.win_valid = win_valid[l];
@@ -902,7 +909,7 @@ int32_t sulimo_hip_execute_prefill_ubatch_ex(
     put(L); put(D); put(F); put(Hq); put(Hkv); put(hd); put((uint64_t)cfg->rope_dim); put(V);
     put((uint64_t)cfg->rope_mode); putf(cfg->rope_base); putf(cfg->eps);
     put(start_pos); put(n); put(cap);
-    putp(ws); put(gemm_ws); putp(lm_panel); putp(tensors->output_norm->dev);
+    putp(ws); put(gemm_ws); putp(lm_panel); putp(tensors->output_norm->dev); putp(attn_ctr);
     for (sulimo_hip_buffer *b : {scratch->x, scratch->h, scratch->q, scratch->k, scratch->v, scratch->attn_out,
                                  scratch->ffn_swiglu, scratch->logits})
       putp(b->dev);

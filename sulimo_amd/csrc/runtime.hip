@@ -50,6 +50,26 @@ int32_t ensure_workspace(sulimo_hip_ctx *ctx, size_t bytes) {
   return SULIMO_HIP_OK;
 }
 
+int32_t ensure_attn_counters(sulimo_hip_ctx *ctx, size_t n, int **out) {
+  *out = nullptr;
+  if (ctx->attn_merge_kernel || n == 0) return SULIMO_HIP_OK;
+  if (ctx->attn_ctr_n < n) {
+    SULIMO_HIP_TRY(hipSetDevice(ctx->device));
+    if (ctx->attn_ctr) {
+      SULIMO_HIP_TRY(hipStreamSynchronize(ctx->stream));
+      SULIMO_HIP_TRY(hipFree(ctx->attn_ctr));
+      ctx->attn_ctr = nullptr;
+      ctx->attn_ctr_n = 0;
+    }
+    const size_t sz = (n + 1023) & ~(size_t)1023;
+    SULIMO_HIP_TRY(hipMalloc(&ctx->attn_ctr, sz * sizeof(int)));
+    SULIMO_HIP_TRY(hipMemsetAsync(ctx->attn_ctr, 0, sz * sizeof(int), ctx->stream));
+    ctx->attn_ctr_n = sz;
+  }
+  *out = ctx->attn_ctr;
+  return SULIMO_HIP_OK;
+}
+
 int prof_begin(sulimo_hip_ctx *ctx) {
   if (!ctx->prof) return -1;
   const int i = (int)ctx->pending.size();
@@ -296,6 +316,7 @@ int32_t sulimo_hip_context_release(sulimo_hip_ctx *ctx) {
   hipStreamSynchronize(ctx->stream);
   if (ctx->ws) hipFree(ctx->ws);
   if (ctx->tok) hipFree(ctx->tok);
+  if (ctx->attn_ctr) hipFree(ctx->attn_ctr);
   hipStreamSynchronize(ctx->side);
   hipEventDestroy(ctx->done_event);
   hipEventDestroy(ctx->near_event);
@@ -350,6 +371,14 @@ int32_t sulimo_hip_set_graph_replay(sulimo_hip_ctx *ctx, int32_t enable) {
   if (rc) return rc;
   ctx->graph_replay = enable != 0;
   if (!ctx->graph_replay) drop_prefill_graphs(ctx);
+  return SULIMO_HIP_OK;
+}
+
+int32_t sulimo_hip_set_attention_merge_kernel(sulimo_hip_ctx *ctx, int32_t enable) {
+  if (!ctx) return fail(SULIMO_HIP_ERR_INVALID_ARGUMENT, "ctx is null");
+  int32_t rc = sulimo_hip_wait(ctx);
+  if (rc) return rc;
+  ctx->attn_merge_kernel = enable != 0;
   return SULIMO_HIP_OK;
 }
 

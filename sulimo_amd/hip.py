@@ -181,6 +181,7 @@ def _declare(L):
         "sulimo_hip_rope_table": (I32, [P, SZ, F, SZ, SZ, P]),
         "sulimo_hip_set_profiling": (I32, [P, I32]),
         "sulimo_hip_set_graph_replay": (I32, [P, I32]),
+        "sulimo_hip_set_attention_merge_kernel": (I32, [P, I32]),
         "sulimo_hip_get_prefill_stats": (I32, [P, C.POINTER(PrefillStats)]),
         "sulimo_hip_timer_start": (I32, [P]),
         "sulimo_hip_timer_stop": (I32, [P, C.POINTER(C.c_float)]),
@@ -247,6 +248,11 @@ class HipContext:
 
     def set_graph_replay(self, enable: bool):
         _check(lib().sulimo_hip_set_graph_replay(self.handle, 1 if enable else 0))
+
+    def set_attention_merge_kernel(self, enable: bool):
+        """Merge split attention blocks in a separate kernel (True) or in the last
+        workgroup to finish each block (False, the default)."""
+        _check(lib().sulimo_hip_set_attention_merge_kernel(self.handle, 1 if enable else 0))
 
     def set_profiling(self, enable: bool):
         """Per-launch hipEvent timing of execute_prefill_ubatch (clears the statistics)."""

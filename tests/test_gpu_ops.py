@@ -216,6 +216,41 @@ def test_attention_prefill_headline_shapes(ctx, hq, hkv, hd, n, cap):
     assert cosine(got, want) >= 0.99999
 
 
+@pytest.mark.parametrize("hq,hkv,hd,n,start,cap", [
+    (12, 2, 128, 2048, 0, 2048),   # the 2048-token prompt's attention
+    (12, 2, 128, 7, 1500, 2048),   # a few queries after a long context: many pieces per block
+    (6, 2, 128, 300, 900, 1024),   # Llama grouping, resumed
+    (4, 4, 64, 200, 2000, 256),    # head_dim 64, ring wrap
+])
+def test_attention_split_merge_paths_bit_identical(ctx, hq, hkv, hd, n, start, cap):
+    """Split query blocks merged by the last workgroup of each block (device-scope
+    record stores and an arrival counter per block and query wave) give the same bits
+    as the separate merge kernel, on three calls in a row (each in-kernel merge leaves
+    its counters at zero for the next call)."""
+    rng = np.random.default_rng(hq * 11 + n + start)
+    q = (3.0 * rng.standard_normal((n, hq, hd))).astype(np.float16)
+    kr, vr = _ring(rng, cap, hkv, hd), _ring(rng, cap, hkv, hd)
+    qb, kb, vb = up(ctx, q), up(ctx, kr), up(ctx, vr)
+    ob = hip.HipBuffer.device_only(ctx, q.nbytes)
+
+    def run():
+        hip.enqueue_attention_prefill(ctx, qb, kb, vb, ob, start, cap, hq, hkv, hd, n)
+        return ob.download(np.float16, q.shape).view(np.uint16).copy()
+
+    try:
+        inkernel = [run() for _ in range(3)]
+        ctx.set_attention_merge_kernel(True)
+        separate = run()
+    finally:
+        ctx.set_attention_merge_kernel(False)
+    for b in (qb, kb, vb, ob):
+        b.release()
+    for r in inkernel:
+        assert np.array_equal(r, separate)
+    want = oracle.attention_prefill_f32(q.astype(np.float32), kr, vr, start, cap, hq, hkv, hd, n).reshape(q.shape)
+    assert max_rel_err(separate.view(np.float16).astype(np.float32), want) <= 1e-2
+
+
 def test_buffer_leak_cycle(ctx):
     """active_cl_mem_count returns to its baseline after create/release cycles
     (test_m4_scheduler.rs:286-365)."""
