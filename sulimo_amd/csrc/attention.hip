@@ -680,10 +680,11 @@ struct AttnPlan {
 
 // Predicted time (us) of one layout, fitted to the measured time of every layout and
 // piece size on MI355X over 17 shapes (Qwen2.5-1.5B, Llama-3.2-3B and a head_dim-64
-// model; prompts of 7 to 4096 tokens at several start positions): the workgroups run in
-// rounds of one per slot (two per CU with one key half, one with two), each round as
-// long as a piece of C steps, fixed + per-step cost; a split block adds ~1 us per piece
-// of the longest split (its last wave merges the pieces).
+// model; prompts of 7 to 4096 tokens at several start positions; its picks checked
+// against a second sweep that timed each plan on a warm clock, in shuffled order): the
+// workgroups run in rounds of one per slot (two per CU with one key half, one with two),
+// each round as long as a piece of C steps, fixed + per-step cost; a split block adds
+// ~1 us per piece of the longest split (its last wave merges the pieces).
 AttnPlan plan_layout(const AttnArgs &a, const Window &w, int halves, int force_c, double *t_out) {
   AttnPlan p;
   p.halves = halves;
@@ -738,8 +739,12 @@ AttnPlan plan_layout(const AttnArgs &a, const Window &w, int halves, int force_c
 AttnPlan plan_attention_uncached(const AttnArgs &a, const Window &w, int halves, int force_c) {
   double t2, t1;
   if (halves) return plan_layout(a, w, halves, force_c, &t2);
-  const AttnPlan p2 = plan_layout(a, w, 2, 0, &t2);
   const AttnPlan p1 = plan_layout(a, w, 1, 0, &t1);
+  // Unsplit blocks of one key half that already fill every slot (two per CU) run best
+  // as they are: splits only add workgroups (Llama-3.2-3B, 4096 tokens: 139.6 us
+  // unsplit against 155-160 us for the best splits and for two key halves).
+  if (p1.n_qblk * a.n_head_kv * p1.n_hgrp >= 2 * device_cu_count()) return plan_layout(a, w, 1, 1 << 30, &t1);
+  const AttnPlan p2 = plan_layout(a, w, 2, 0, &t2);
   return t1 < t2 ? p1 : p2;
 }
 
