@@ -217,7 +217,8 @@ def test_attention_prefill_headline_shapes(ctx, hq, hkv, hd, n, cap):
 
 
 @pytest.mark.parametrize("hq,hkv,hd,n,start,cap", [
-    (12, 2, 128, 2048, 0, 2048),   # the 2048-token prompt's attention
+    (12, 2, 128, 2048, 0, 2048),   # the 2048-token prompt's attention (one key half per workgroup)
+    (12, 2, 128, 512, 1024, 2048),  # third 512-token micro-batch (two key halves per workgroup)
     (12, 2, 128, 7, 1500, 2048),   # a few queries after a long context: many pieces per block
     (6, 2, 128, 300, 900, 1024),   # Llama grouping, resumed
     (4, 4, 64, 200, 2000, 256),    # head_dim 64, ring wrap
