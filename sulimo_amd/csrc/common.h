@@ -302,6 +302,28 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
+// One RMSNorm row held by one wave, lane l holding columns 256 j + 4 l .. +3. Every
+// kernel that normalizes rows this way uses these helpers, so the separate RMSNorm and
+// the one fused into the K-split reduction give identical bits: the sum of squares runs
+// over j in order as one fma chain per lane, then across the wave; the output is the
+// f32 product x * scale * w rounded to f16 once.
+typedef _Float16 rms_half4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float rms_sumsq4(float4 v, float ss) {
+  return __builtin_fmaf(v.w, v.w, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.x, v.x, ss))));
+}
+__device__ __forceinline__ float rms_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float rms_scale(float ss, int d, float eps) { return 1.0f / sqrtf(ss / (float)d + eps); }
+__device__ __forceinline__ rms_half4 rms_out4(float4 v, float scale, float4 w) {
+#pragma clang fp contract(off)
+  float a = v.x * scale * w.x, b = v.y * scale * w.y, c = v.z * scale * w.z, d = v.w * scale * w.w;
+  asm("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));  // no fused product-and-round (v_fma_mix)
+  return rms_half4{(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)d};
+}
+
 // Compute units of the current device (cached per device).
 int device_cu_count();
 

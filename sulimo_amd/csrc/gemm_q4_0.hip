@@ -1083,17 +1083,13 @@ __global__ __launch_bounds__(256) void split_reduce_norm_vec_kernel(GemmArgs a) 
     v[j] = nx;
   }
 #pragma unroll
-  for (int j = 0; j < V; j++) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  const float scale = 1.0f / sqrtf(ss / (float)D + a.norm_eps);
+  for (int j = 0; j < V; j++) ss = rms_sumsq4(v[j], ss);
+  const float scale = rms_scale(rms_wave_sum(ss), D, a.norm_eps);
   _Float16 *out = reinterpret_cast<_Float16 *>(a.norm_out) + (size_t)row * D;
 #pragma unroll
   for (int j = 0; j < V; j++) {
     const int c = 256 * j + 4 * lane;
-    const float4 wv = nw[j];
-    *reinterpret_cast<half4v *>(out + c) = half4v{(_Float16)(v[j].x * scale * wv.x), (_Float16)(v[j].y * scale * wv.y),
-                                                  (_Float16)(v[j].z * scale * wv.z), (_Float16)(v[j].w * scale * wv.w)};
+    *reinterpret_cast<rms_half4 *>(out + c) = rms_out4(v[j], scale, nw[j]);
     if (a.norm_x16)
       *reinterpret_cast<half4v *>(reinterpret_cast<_Float16 *>(a.norm_x16) + (size_t)row * D + c) =
           half4v{(_Float16)v[j].x, (_Float16)v[j].y, (_Float16)v[j].z, (_Float16)v[j].w};

@@ -55,16 +55,12 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const T *__restrict__ 
     wl[j] = *reinterpret_cast<const float4 *>(w + 256 * j + 4 * lane);
   }
 #pragma unroll
-  for (int j = 0; j < V; j++) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
-  ss = wave_sum(ss);
-  const float scale = 1.0f / sqrtf(ss / (float)D + eps);
+  for (int j = 0; j < V; j++) ss = rms_sumsq4(v[j], ss);
+  const float scale = rms_scale(rms_wave_sum(ss), D, eps);
 #pragma unroll
   for (int j = 0; j < V; j++) {
     const int i = 256 * j + 4 * lane;
-    const float4 wv = wl[j];
-    const half4v o = {(_Float16)(v[j].x * scale * wv.x), (_Float16)(v[j].y * scale * wv.y),
-                      (_Float16)(v[j].z * scale * wv.z), (_Float16)(v[j].w * scale * wv.w)};
-    *reinterpret_cast<half4v *>(out + (size_t)row * D + i) = o;
+    *reinterpret_cast<rms_half4 *>(out + (size_t)row * D + i) = rms_out4(v[j], scale, wl[j]);
     if (x16_out) {
       const half4v h = {(_Float16)v[j].x, (_Float16)v[j].y, (_Float16)v[j].z, (_Float16)v[j].w};
       *reinterpret_cast<half4v *>(x16_out + (size_t)row * D + i) = h;
