@@ -102,13 +102,16 @@ def traffic_from_profiles(key: str):
 
 
 def gemm_table(ctx, hip, S):
-    """TFLOP/s of each Q4_0 linear of one Qwen2.5-1.5B layer at M=512 and of the
-    up-projection at M=128, hipEvent-timed over 20 back-to-back launches."""
+    """TFLOP/s of each Q4_0 linear of one Qwen2.5-1.5B layer at M=512, of the
+    up-projection at M=128, 2048 and 4096 and of the Llama-3.2-3B up-projection at
+    M=4096 (whole rounds of tiles: the kernel's rate without a partial last round),
+    hipEvent-timed over 20 back-to-back launches."""
     rng = np.random.default_rng(0x5EED0001)
     shapes = [("q_proj", 512, 1536, 1536), ("k_proj", 512, 1536, 256), ("v_proj", 512, 1536, 256),
               ("o_proj", 512, 1536, 1536), ("gate_proj", 512, 1536, 8960), ("up_proj", 512, 1536, 8960),
               ("down_proj", 512, 8960, 1536), ("up_proj_m128", 128, 1536, 8960),
-              ("lm_head_m1", 1, 1536, 151936)]
+              ("up_proj_m2048", 2048, 1536, 8960), ("up_proj_m4096", 4096, 1536, 8960),
+              ("llama3b_up_proj_m4096", 4096, 3072, 8192), ("lm_head_m1", 1, 1536, 151936)]
     out = {}
     tot_flop, tot_ms = 0.0, 0.0
     for name, M, K, N in shapes:
@@ -116,9 +119,14 @@ def gemm_table(ctx, hip, S):
         x = rng.standard_normal((M, K)).astype(np.float16)
         bufs = [hip.HipBuffer.from_host(ctx, w.scales, True), hip.HipBuffer.from_host(ctx, w.quants, True),
                 hip.HipBuffer.from_host(ctx, x, True), hip.HipBuffer.device_only(ctx, M * N * 2)]
-        for _ in range(3):
-            hip.enqueue_gemm_q4_0_f16(ctx, *bufs, N, K, M)
+        # warm: at least 30 ms of this shape, so that the clock has left the previous
+        # shape's level
         ctx.wait()
+        tw = time.perf_counter()
+        while time.perf_counter() - tw < 0.03:
+            for _ in range(10):
+                hip.enqueue_gemm_q4_0_f16(ctx, *bufs, N, K, M)
+            ctx.wait()
         it = 20
         ctx.timer_start()
         for _ in range(it):
